@@ -1,0 +1,227 @@
+// Internal declarations shared by the runtime, the graph executor and the kernel launchers of
+// the MI355X backend. Nothing here crosses the C ABI (see include/mxrt.h for that).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/mxrt.h"
+
+namespace mx {
+
+// ------------------------------------------------------------------------------------------
+// Errors: thread-local last message + status code.
+// ------------------------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+#define MX_CHECK_HIP(expr)                                                                  \
+  do {                                                                                      \
+    hipError_t e__ = (expr);                                                                \
+    if (e__ != hipSuccess)                                                                  \
+      return ::mx::set_error(MX_ERR_HIP, "%s failed: %s (%s:%d)", #expr,                    \
+                             hipGetErrorString(e__), __FILE__, __LINE__);                   \
+  } while (0)
+
+#define MX_TRY(expr)                 \
+  do {                               \
+    int rc__ = (expr);               \
+    if (rc__ != MX_OK) return rc__;  \
+  } while (0)
+
+// ------------------------------------------------------------------------------------------
+// DTypes (values of dtypes.DType, dtypes/dtype_enum.go:20-140).
+// ------------------------------------------------------------------------------------------
+bool dtype_known(int dt);
+const char* dtype_name(int dt);
+int dtype_bits(int dt);             // 4 for Int4/Uint4, 8*size otherwise; 0 if unknown
+bool dtype_is_float(int dt);        // F16, BF16, F32, F64
+bool dtype_is_half(int dt);         // F16, BF16
+bool dtype_is_int(int dt);          // signed/unsigned integers incl. packed
+bool dtype_is_packed(int dt);       // Int4/Uint4
+
+struct Shape {
+  int dtype = MX_DTYPE_INVALID;
+  std::vector<int64_t> dims;
+  int rank() const { return (int)dims.size(); }
+  int64_t size() const {
+    int64_t n = 1;
+    for (auto d : dims) n *= d;
+    return n;
+  }
+  // Storage bytes; packed dtypes round up to whole bytes (dtypes.go:221-239).
+  size_t nbytes() const {
+    int64_t n = size();
+    int b = dtype_bits(dtype);
+    return (size_t)((n * b + 7) / 8);
+  }
+  bool operator==(const Shape& o) const { return dtype == o.dtype && dims == o.dims; }
+  bool operator!=(const Shape& o) const { return !(*this == o); }
+  std::string str() const;
+};
+
+int shape_from_c(const mx_shape* s, Shape* out);
+void shape_to_c(const Shape& s, mx_shape* out);
+
+// ------------------------------------------------------------------------------------------
+// Device context.
+// ------------------------------------------------------------------------------------------
+
+// Caching allocator over hipMalloc.  All device work of a backend runs on one stream, so a
+// block returned to the pool may be handed out again immediately: any later use is ordered
+// after the earlier use on that stream.
+class DevicePool {
+ public:
+  int alloc(size_t bytes, void** out);  // MX_OK or MX_ERR_OUT_OF_MEMORY / MX_ERR_HIP
+  void release(void* p);
+  void trim();                           // hipFree all cached blocks
+  void destroy();                        // hipFree everything (backend finalize)
+  int fail_after = 0;                    // fault injection: n-th alloc fails (0 = off)
+  size_t bytes_in_use() const { return in_use_; }
+  size_t bytes_cached() const { return cached_; }
+
+ private:
+  static size_t round_size(size_t b);
+  std::unordered_map<void*, size_t> live_;         // ptr -> rounded size
+  std::multimap<size_t, void*> free_;              // rounded size -> ptr
+  size_t in_use_ = 0, cached_ = 0;
+};
+
+struct ProfEntry {
+  int64_t launches = 0;
+  double total_ms = 0.0;
+};
+
+struct PendingTiming {
+  std::string name;
+  hipEvent_t start, stop;
+};
+
+}  // namespace mx
+
+struct mx_backend {
+  int device = 0;
+  bool host_only = false;
+  bool finalized = false;
+  hipStream_t stream = nullptr;
+  std::recursive_mutex mu;
+  mx::DevicePool pool;
+  std::string description;
+  int num_cus = 0;
+  int xcds = 8;
+
+  // Scratch for split-K partial sums and arrival counters. Counters are kept at zero between
+  // launches (the last workgroup of a tile resets its counter), so the buffer is cleared only
+  // when it is (re)allocated.
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+
+  // Profiling.
+  bool profiling = false;
+  std::vector<mx::PendingTiming> pending;
+  std::vector<hipEvent_t> event_cache;
+  std::map<std::string, mx::ProfEntry> prof;
+
+  int64_t live_buffers = 0;
+};
+
+struct mx_buffer {
+  mx_backend* b = nullptr;
+  mx::Shape shape;
+  void* dptr = nullptr;
+  size_t nbytes = 0;
+  bool finalized = false;
+};
+
+namespace mx {
+
+// Checks the backend can run device work.
+int check_device(mx_backend* b);
+// Allocate/free device memory from the backend's pool.
+int dev_alloc(mx_backend* b, size_t bytes, void** out);
+void dev_free(mx_backend* b, void* p);
+// Ensures scratch has at least `bytes` (zero-filled on growth). Returns the device pointer.
+int ensure_scratch(mx_backend* b, size_t bytes, void** out);
+
+// Launch wrapper: records a hipEvent pair around the launch when profiling is on, and checks
+// the launch status.
+template <typename F>
+int launch(mx_backend* b, const char* name, F&& fn);
+
+int timing_begin(mx_backend* b, hipEvent_t* start);
+int timing_end(mx_backend* b, const char* name, hipEvent_t start);
+
+template <typename F>
+int launch(mx_backend* b, const char* name, F&& fn) {
+  hipEvent_t ev = nullptr;
+  if (b->profiling) MX_TRY(timing_begin(b, &ev));
+  fn();
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(MX_ERR_HIP, "launch of %s failed: %s", name, hipGetErrorString(e));
+  if (b->profiling) MX_TRY(timing_end(b, name, ev));
+  return MX_OK;
+}
+
+// ------------------------------------------------------------------------------------------
+// Kernel launchers (implemented in the .hip files).
+// ------------------------------------------------------------------------------------------
+
+// Validated description of one FusedQuantizedDense call on device pointers.
+struct QDenseDesc {
+  const void* x;
+  const void* w;
+  const void* scale;
+  const void* zp;
+  const void* bias;
+  void* out;
+  int64_t M, K, N;
+  int x_dt, w_dt, s_dt, zp_dt, b_dt;
+  int scheme, block_axis, block_size, act;
+};
+int qdense_validate(const mx_qdense_args* a, QDenseDesc* d);
+int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name);
+int qdense_run(mx_backend* b, const QDenseDesc& d);
+
+// Normalized DotGeneral: out[b, m, n] = sum_k lhs[b, m, k] * rhs[b, k, n] (or rhs[b, n, k] when
+// rhs_transposed).
+struct DotDesc {
+  const void* lhs;
+  const void* rhs;
+  void* out;
+  int64_t B, M, K, N;
+  bool rhs_transposed;
+  int in_dt, out_dt;  // out_dt: F32 for half inputs, else in_dt (conversion handled by caller)
+};
+int dot_run(mx_backend* b, const DotDesc& d);
+
+// Elementwise / data-movement kernels (elementwise.hip).
+int ew_convert(mx_backend* b, const void* in, int in_dt, void* out, int out_dt, int64_t n);
+int ew_unary(mx_backend* b, int optype, const void* in, void* out, int dt, int64_t n);
+// Binary op with broadcasting: both operands are viewed with out's rank; a dimension of size 1
+// broadcasts.  lhs_dims/rhs_dims have `rank` entries.
+int ew_binary(mx_backend* b, int optype, const void* lhs, const int64_t* lhs_dims,
+              const void* rhs, const int64_t* rhs_dims, void* out, const int64_t* out_dims,
+              int rank, int dt);
+// out = in with strided gather: out[idx] = in[sum_i idx_i * in_strides[i] + offset].  Covers
+// Transpose, BroadcastInDim (stride 0) and Slice.
+int ew_gather_strided(mx_backend* b, const void* in, void* out, int elem_bytes,
+                      const int64_t* out_dims, const int64_t* in_strides, int64_t in_offset,
+                      int rank);
+// Reduction over a set of axes (reduce_mask bit i set = axis i reduced).
+int ew_reduce(mx_backend* b, int optype, const void* in, void* out, int dt,
+              const int64_t* dims, int rank, uint32_t reduce_mask);
+int ew_iota(mx_backend* b, void* out, int dt, const int64_t* dims, int rank, int axis);
+int ew_bias_act(mx_backend* b, const void* in, void* out, int dt, const void* bias, int64_t rows,
+                int64_t cols, int act);
+int ew_gelu(mx_backend* b, const void* in, void* out, int dt, int64_t n, int exact);
+
+}  // namespace mx

@@ -1,0 +1,209 @@
+"""C-ABI and host-logic tests (no GPU needed).
+
+- libmxrt.so loads and exports every function include/mxrt.h declares;
+- graph building on a host_only backend: shape inference and the validation errors of
+  FusedQuantizedDense (quantizeddense.go:92-130) and DotGeneral (dotgeneral.go:16-152), value
+  ownership across builders, NotImplemented for unsupported configurations, and that every
+  device operation fails loudly (no host fallback).
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import compute_amd as ca
+from compute_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    text = open(os.path.join(ROOT, "include", "mxrt.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    names = _declared_functions()
+    assert len(names) >= 50
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding declares a signature for each of them
+    assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
+
+
+def test_backend_identity(host_backend):
+    b = host_backend
+    assert b.Name() == "mi355x"
+    assert "MI355X" in b.Description()
+    assert b.NumDevices() == 0
+    assert not b.HasSharedBuffers()
+    caps = b.Capabilities()
+    assert caps.Operations.get(ca.OpType.FusedQuantizedDense)
+    assert caps.Operations.get(ca.OpType.DotGeneral)
+    assert not caps.Operations.get(ca.OpType.FusedScaledDotProductAttention, False)
+    assert caps.DTypes.get(ca.BFloat16) and caps.DTypes.get(ca.Int4)
+
+
+def test_bad_config_rejected():
+    with pytest.raises(ca.ComputeError):
+        ca.New("mi355x:frobnicate")
+
+
+def test_device_operations_fail_loudly_host_only(host_backend):
+    with pytest.raises(ca.ErrNoDevice):
+        host_backend.BufferFromFlatData(0, np.zeros(4, np.float32), ca.Shape(ca.Float32, 4))
+    with pytest.raises(ca.ErrNoDevice):
+        host_backend.Synchronize()
+
+
+def _qd_builder(b, xs, ws, ss, bias_shape=None):
+    bld = b.Builder("qd")
+    f = bld.Main()
+    x = f.Parameter("x", xs)
+    w = f.Parameter("w", ws)
+    s = f.Parameter("s", ss)
+    bias = f.Parameter("bias", bias_shape) if bias_shape else None
+    return bld, f, x, w, s, bias
+
+
+def test_qdense_shape_inference(host_backend):
+    bld, f, x, w, s, bias = _qd_builder(host_backend, ca.Shape(ca.BFloat16, 2, 3, 64), ca.Shape(ca.Int4, 64, 40),
+                                        ca.Shape(ca.BFloat16, 2, 40), ca.Shape(ca.BFloat16, 40))
+    y = f.FusedQuantizedDense(x, w, bias, ca.Quantization(ca.QuantLinear, s, None, 0, 32), ca.ActivationSilu)
+    assert f.Shape(y) == ca.Shape(ca.BFloat16, 2, 3, 40)
+    assert bld.OpShape(y) == ca.Shape(ca.BFloat16, 2, 3, 40)
+    f.Return([y])
+    exe = bld.Compile()
+    names, shapes = exe.Inputs()
+    assert names == ["x", "w", "s", "bias"]
+    assert exe.Outputs() == [ca.Shape(ca.BFloat16, 2, 3, 40)]
+
+
+def test_qdense_reference_layout_and_per_channel_vector(host_backend):
+    # Reference layout: BlockAxis=1, scale [K, ceil(N/B)] with a ragged last block.
+    _, f, x, w, s, _ = _qd_builder(host_backend, ca.Shape(ca.Float32, 4, 16), ca.Shape(ca.Int8, 16, 10),
+                                   ca.Shape(ca.Float32, 16, 3))
+    y = f.FusedQuantizedDense(x, w, None, ca.Quantization(ca.QuantLinear, s, None, 1, 4), ca.ActivationNone)
+    assert f.Shape(y) == ca.Shape(ca.Float32, 4, 10)
+    # Per-output-channel scale given as [N].
+    _, f, x, w, s, _ = _qd_builder(host_backend, ca.Shape(ca.Float32, 4, 16), ca.Shape(ca.Int8, 16, 10),
+                                   ca.Shape(ca.Float32, 10))
+    y = f.FusedQuantizedDense(x, w, None, ca.Quantization(ca.QuantLinear, s, None, 0, 16), ca.ActivationGelu)
+    assert f.Shape(y) == ca.Shape(ca.Float32, 4, 10)
+
+
+@pytest.mark.parametrize("case", ["wrongK", "scales", "bias", "axis", "nf4zp", "xint", "wfloat", "blocksize"])
+def test_qdense_validation_errors(host_backend, case):
+    b = host_backend
+    bld = b.Builder("bad")
+    f = bld.Main()
+    x = f.Parameter("x", ca.Shape(ca.Int32 if case == "xint" else ca.Float32, 2, 16))
+    w = f.Parameter("w", ca.Shape(ca.Float32 if case == "wfloat" else ca.Int8, 8 if case == "wrongK" else 16, 12))
+    s = f.Parameter("s", ca.Shape(ca.Float32, 16, 5 if case == "scales" else 3))
+    zp = f.Parameter("zp", ca.Shape(ca.Float32, 16, 3))
+    bias = f.Parameter("b", ca.Shape(ca.Float32, 11 if case == "bias" else 12))
+    q = ca.Quantization(ca.QuantNF4 if case == "nf4zp" else ca.QuantLinear, s, zp if case == "nf4zp" else None,
+                        2 if case == "axis" else 1, 0 if case == "blocksize" else 4)
+    expect = ca.ErrNotImplemented if case in ("xint", "wfloat") else ca.ComputeError
+    with pytest.raises(expect) as ei:
+        f.FusedQuantizedDense(x, w, bias, q, ca.ActivationNone)
+    if expect is ca.ComputeError:
+        assert not ca.IsNotImplemented(ei.value)
+
+
+def test_qdense_ggml_not_implemented(host_backend):
+    _, f, x, w, s, _ = _qd_builder(host_backend, ca.Shape(ca.Float32, 1, 32), ca.Shape(ca.Uint8, 4, 18),
+                                   ca.Shape(ca.Float32, 1))
+    with pytest.raises(ca.ErrNotImplemented):
+        f.FusedQuantizedDense(x, w, None, ca.Quantization(ca.QuantGGML, s, None, 1, 1), ca.ActivationNone)
+
+
+def test_values_from_other_builder_rejected(host_backend):
+    b1 = host_backend.Builder("one")
+    b2 = host_backend.Builder("two")
+    x1 = b1.Main().Parameter("x", ca.Shape(ca.Float32, 3))
+    f2 = b2.Main()
+    x2 = f2.Parameter("x", ca.Shape(ca.Float32, 3))
+    with pytest.raises(ca.ComputeError, match="different builder"):
+        f2.Add(x1, x2)
+
+
+def test_return_then_modify_and_compile_rules(host_backend):
+    bld = host_backend.Builder("r")
+    f = bld.Main()
+    x = f.Parameter("x", ca.Shape(ca.Float32, 3))
+    f.Return([x])
+    with pytest.raises(ca.ComputeError):
+        f.Neg(x)
+    bld.Compile()
+    bld2 = host_backend.Builder("no-return")
+    bld2.Main().Parameter("x", ca.Shape(ca.Float32, 3))
+    with pytest.raises(ca.ComputeError, match="Return"):
+        bld2.Compile()
+
+
+def test_dot_general_shape_kat(host_backend):
+    # support/backendtest/dotgeneral.go:26-81
+    bld = host_backend.Builder("DotGeneral Test")
+    f = bld.Main()
+    lhs = f.Parameter("lhs", ca.Shape(ca.Float32, 2, 3, 4, 5))
+    rhs = f.Parameter("rhs", ca.Shape(ca.Float32, 5, 1, 2, 3))
+    y = f.DotGeneral(lhs, [1], [3, 0], rhs, [3], [0, 2])
+    assert f.Shape(y) == ca.Shape(ca.Float32, 5, 2, 4, 1)
+    y2 = f.DotGeneral(lhs, [1], [3, 0], rhs, [3], [0, 2], ca.DotGeneralConfig(OutputDType=ca.Float64))
+    assert f.Shape(y2) == ca.Shape(ca.Float64, 5, 2, 4, 1)
+
+
+@pytest.mark.parametrize("case", ["dtype", "ncontract", "dim", "reuse", "range"])
+def test_dot_general_errors(host_backend, case):
+    f = host_backend.Builder("e").Main()
+    lhs = f.Parameter("l", ca.Shape(ca.Float32, 2, 3))
+    rhs = f.Parameter("r", ca.Shape(ca.Float64 if case == "dtype" else ca.Float32, 4 if case == "dim" else 3, 5))
+    args = {
+        "dtype": ([1], [], [0], []), "ncontract": ([1], [], [0, 1], []), "dim": ([1], [], [0], []),
+        "reuse": ([1, 1], [], [0, 1], []), "range": ([2], [], [0], []),
+    }[case]
+    with pytest.raises(ca.ComputeError):
+        f.DotGeneral(lhs, args[0], args[1], rhs, args[2], args[3])
+
+
+def test_binary_broadcast_rules(host_backend):
+    f = host_backend.Builder("bin").Main()
+    a = f.Parameter("a", ca.Shape(ca.BFloat16, 8, 1))
+    b = f.Parameter("b", ca.Shape(ca.BFloat16, 8, 4096))
+    s = f.Parameter("s", ca.Shape(ca.BFloat16))
+    assert f.Shape(f.Mul(a, b)) == ca.Shape(ca.BFloat16, 8, 4096)
+    assert f.Shape(f.Add(s, b)) == ca.Shape(ca.BFloat16, 8, 4096)
+    c = f.Parameter("c", ca.Shape(ca.BFloat16, 4096))
+    with pytest.raises(ca.ComputeError):
+        f.Add(b, c)  # different rank, neither scalar
+    d = f.Parameter("d", ca.Shape(ca.Float32, 8, 4096))
+    with pytest.raises(ca.ComputeError):
+        f.Add(b, d)  # dtype mismatch
+
+
+def test_shape_ops_inference(host_backend):
+    f = host_backend.Builder("shapes").Main()
+    x = f.Parameter("x", ca.Shape(ca.Uint8, 6, 4))
+    assert f.Shape(f.Bitcast(x, ca.Int4)) == ca.Shape(ca.Int4, 6, 4, 2)
+    assert f.Shape(f.Reshape(f.Bitcast(x, ca.Int4), 6, 8)) == ca.Shape(ca.Int4, 6, 8)
+    y = f.Parameter("y", ca.Shape(ca.Float32, 2, 3, 4))
+    assert f.Shape(f.Transpose(y, 2, 0, 1)) == ca.Shape(ca.Float32, 4, 2, 3)
+    assert f.Shape(f.ReduceSum(y, 1)) == ca.Shape(ca.Float32, 2, 4)
+    assert f.Shape(f.ReduceSum(y)) == ca.Shape(ca.Float32)
+    assert f.Shape(f.Slice(y, [0, 1, 0], [2, 3, 4], [1, 1, 2])) == ca.Shape(ca.Float32, 2, 2, 2)
+    v = f.Parameter("v", ca.Shape(ca.Float32, 3))
+    assert f.Shape(f.BroadcastInDim(v, ca.Shape(ca.Float32, 2, 3), [1])) == ca.Shape(ca.Float32, 2, 3)
+    assert f.Shape(f.Iota(ca.Shape(ca.Float32, 16), 0)) == ca.Shape(ca.Float32, 16)
+    with pytest.raises(ca.ComputeError):
+        f.Reshape(y, 5, 5)
+
+
+def test_fault_injection_flag_is_host_side(host_backend):
+    # The knob is set on the host; the allocation it fails happens only on a device backend.
+    host_backend.DebugFailAllocAfter(1)
+    host_backend.DebugFailAllocAfter(0)
