@@ -10,6 +10,25 @@
 namespace mx {
 
 // ---------------------------------------------------------------------------------------------
+// Single-rounded f32 arithmetic that is never contracted into an FMA.  HIP's __fadd_rn and
+// __fmul_rn are plain `+`/`*` here (no OCML rounded operations), which clang fuses into FMAs
+// under its default -ffp-contract for HIP; the reference's Go loops round every product and sum
+// separately, so reference-order code uses these instead.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float div_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a / b;
+}
+
+// ---------------------------------------------------------------------------------------------
 // bf16 <-> f32.  f32 -> bf16 follows bfloat16.FromFloat32 (dtypes/bfloat16/bfloat16.go:30-39):
 // NaN/Inf keep their top 16 bits, everything else rounds to nearest even.
 // ---------------------------------------------------------------------------------------------
@@ -82,29 +101,54 @@ __device__ __forceinline__ float act_ref(float x, int act) {
   switch (act) {
     case MX_ACT_GELU: {
       // x * 0.5 * (1 + float32(erf(float64(x * float32(1/sqrt(2))))))
-      float t = __fmul_rn(x, __uint_as_float(0x3f3504f3u));
+      float t = mul_rn(x, __uint_as_float(0x3f3504f3u));
       float e = (float)erf((double)t);
-      return __fmul_rn(__fmul_rn(x, 0.5f), __fadd_rn(1.0f, e));
+      return mul_rn(mul_rn(x, 0.5f), add_rn(1.0f, e));
     }
     case MX_ACT_RELU:
       return x < 0.0f ? 0.0f : x;
     case MX_ACT_SILU: {
       float e = (float)exp((double)(-x));
-      return __fdiv_rn(x, __fadd_rn(1.0f, e));
+      return div_rn(x, add_rn(1.0f, e));
     }
     case MX_ACT_HARDSWISH: {
       // shapeX := min(max(x*float32(1/6) + 0.5, 0), 1); x * shapeX  (Go min/max propagate NaN)
-      float v = __fadd_rn(__fmul_rn(x, __uint_as_float(0x3e2aaaabu)), 0.5f);
+      float v = add_rn(mul_rn(x, __uint_as_float(0x3e2aaaabu)), 0.5f);
       if (v != v) return v;
       v = v > 0.0f ? v : 0.0f;
       v = v < 1.0f ? v : 1.0f;
-      return __fmul_rn(x, v);
+      return mul_rn(x, v);
     }
     case MX_ACT_TANH:
       return (float)tanh((double)x);
     default:
       return x;
   }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Split-K completion: every workgroup that owns one K slice of a tile calls this after storing
+// its partial results; it returns true (in all threads) only in the workgroup that arrives
+// last, which may then read every slice's partials and finish the tile.
+//
+// Cost matters here: an agent-scope fence on gfx950 writes back (release) or invalidates
+// (acquire) the whole L2 of the XCD.  So the workgroup barrier first orders the other waves'
+// stores before thread 0's single release RMW, and only the last arriver acquires.  The counter
+// is reset for the next launch by the last arriver (no other workgroup touches it afterwards).
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ bool splitk_last_arriver(uint32_t* counter, uint32_t arrivals, int* s_flag) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == arrivals - 1u;
+    if (last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *s_flag = last;
+  }
+  __syncthreads();
+  return *s_flag != 0;
 }
 
 }  // namespace mx

@@ -440,7 +440,7 @@ __global__ void bias_act_kernel(const void* in, void* out, int dt, const void* b
       ((double*)out)[i] = act_f64(v, act);
     } else {
       float v = load_f(in, i, dt);
-      if (bias) v = __fadd_rn(v, load_f(bias, c, dt));
+      if (bias) v = add_rn(v, load_f(bias, c, dt));
       store_f(out, i, dt, act_ref(v, act));
     }
   }
@@ -472,8 +472,8 @@ __global__ void gelu_kernel(const void* in, void* out, int dt, int64_t n, int ex
       r = act_ref(x, MX_ACT_GELU);
     } else {
       // x * 0.5 * (1 + float32(tanh(float64(sqrt(2/pi) * (x + 0.044715*x*x*x)))))  (gelu.go:120-126)
-      const float inner = __fmul_rn(0.7978846f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
-      r = __fmul_rn(__fmul_rn(x, 0.5f), __fadd_rn(1.0f, (float)tanh((double)inner)));
+      const float inner = mul_rn(0.7978846f, add_rn(x, mul_rn(mul_rn(mul_rn(0.044715f, x), x), x)));
+      r = mul_rn(mul_rn(x, 0.5f), add_rn(1.0f, (float)tanh((double)inner)));
     }
     if (dt == MX_DTYPE_FLOAT32) ((float*)out)[i] = r;
     else if (dt == MX_DTYPE_BFLOAT16) ((uint16_t*)out)[i] = f32_to_bf16(r);

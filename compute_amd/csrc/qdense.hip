@@ -102,15 +102,15 @@ __global__ __launch_bounds__(kExactThreads) void qdense_exact_kernel(QDenseDesc 
     const float wf = d.scheme == MX_QUANT_NF4 ? kNF4Table[(uint32_t)wi & 15u] : (float)wi;
     if (d.zp) {
       const float z = load_f(d.zp, si, d.zp_dt);
-      const float u = __fadd_rn(__fmul_rn(wf, s), z);
+      const float u = add_rn(mul_rn(wf, s), z);
 #pragma unroll
       for (int r = 0; r < kExactRows; ++r)
-        if (r < rows) acc[r] = __fadd_rn(acc[r], __fmul_rn(load_f(d.x, (m0 + r) * K + k, d.x_dt), u));
+        if (r < rows) acc[r] = add_rn(acc[r], mul_rn(load_f(d.x, (m0 + r) * K + k, d.x_dt), u));
     } else {
 #pragma unroll
       for (int r = 0; r < kExactRows; ++r)
         if (r < rows)
-          acc[r] = __fadd_rn(acc[r], __fmul_rn(__fmul_rn(load_f(d.x, (m0 + r) * K + k, d.x_dt), wf), s));
+          acc[r] = add_rn(acc[r], mul_rn(mul_rn(load_f(d.x, (m0 + r) * K + k, d.x_dt), wf), s));
     }
   }
 #pragma unroll
@@ -294,22 +294,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_dot2_kernel(GemvArgs a) {
   }
 
   if (t < kCB) a.partial[(size_t)slice * a.N + n] = v;
-  __threadfence();
-  __syncthreads();
-  if (t == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&a.counters[cb], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (uint32_t)(a.S - 1)) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!splitk_last_arriver(&a.counters[cb], (uint32_t)a.S, &s_last)) return;
   if (t < kCB) {
     float y = 0.0f;
-    for (int s = 0; s < a.S; ++s) y += __builtin_nontemporal_load(&a.partial[(size_t)s * a.N + n]);
+    for (int s = 0; s < a.S; ++s) y += a.partial[(size_t)s * a.N + n];
     if (a.bias) y += load_f(a.bias, n, a.b_dt);
     a.out[n] = f32_to_bf16(act_ref(y, a.act));
   }
-  if (t == 0) __hip_atomic_store(&a.counters[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // =============================================================================================
