@@ -126,6 +126,30 @@ __device__ __forceinline__ float act_ref(float x, int act) {
   }
 }
 
+// Activation epilogue of the fast kernels, in f32 (OCML erff/tanhf, hardware exp): within a few
+// f32 ulps of act_ref, far below the bf16 rounding of their outputs.
+__device__ __forceinline__ float act_fast(float x, int act) {
+  switch (act) {
+    case MX_ACT_GELU:
+      return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+    case MX_ACT_RELU:
+      return x < 0.0f ? 0.0f : x;
+    case MX_ACT_SILU:
+      return x / (1.0f + __expf(-x));
+    case MX_ACT_HARDSWISH: {
+      float v = x * (1.0f / 6.0f) + 0.5f;
+      if (v != v) return v;
+      v = v > 0.0f ? v : 0.0f;
+      v = v < 1.0f ? v : 1.0f;
+      return x * v;
+    }
+    case MX_ACT_TANH:
+      return tanhf(x);
+    default:
+      return x;
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Split-K completion: every workgroup that owns one K slice of a tile calls this after storing
 // its partial results; it returns true (in all threads) only in the workgroup that arrives

@@ -190,6 +190,9 @@ struct QDenseDesc {
 int qdense_validate(const mx_qdense_args* a, QDenseDesc* d);
 int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name);
 int qdense_run(mx_backend* b, const QDenseDesc& d);
+// Skinny-M MFMA kernel (qdense_skinny.hip): shape/layout check and launch.
+bool qdense_skinny_fits(const QDenseDesc& d);
+int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name);
 
 // Normalized DotGeneral: out[b, m, n] = sum_k lhs[b, m, k] * rhs[b, k, n] (or rhs[b, n, k] when
 // rhs_transposed).

@@ -1,0 +1,98 @@
+"""Skinny-M FusedQuantizedDense (decode and small batches, M <= 16 bf16 rows) on the GPU vs the
+CPU oracle.
+
+The kernel sums in another order than the reference loop (per-group partial sums on the matrix
+cores, the group scale applied once per group, split-K partials added in slice order), so:
+  - bf16 outputs must be within rel 1e-2 / abs 1e-3 of the oracle's f32 result;
+  - the pre-rounding f32 accumulation must be within 1e-5 of sum|terms| of the exact (f64)
+    value, checked through the bf16 output (half an ulp of bf16, 2^-9 relative, is allowed on
+    top);
+  - two calls on the same inputs must return identical bits (deterministic reduction).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.qd_helpers import QDenseRun, assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+
+W_DTYPES = [O.DT_INT8, O.DT_UINT8, O.DT_INT4, O.DT_UINT4]
+
+
+def check(r: QDenseRun, threads: int = 1, what: str = ""):
+    p = r.p
+    y = r.run()
+    assert_bf16_close(y, O.qdense_f32(p, threads=threads), what=what)
+    if p.act == O.ACT_NONE:
+        truth = O.qdense_f64(p)
+        scale = O.qdense_f64(p, absolute=True)
+        got = O.bf16_to_f32(y).astype(np.float64)
+        assert np.all(np.abs(got - truth) <= 2.0 ** -8 * np.abs(truth) + 1e-5 * scale), what
+    y2 = r.run()
+    assert np.array_equal(y, y2), f"{what}: not deterministic"
+    return y
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 16])
+@pytest.mark.parametrize("w_dtype", W_DTYPES)
+def test_skinny_rows_and_dtypes(backend, M, w_dtype):
+    p = O.make_problem(M, 512, 768, w_dtype=w_dtype, block_axis=0, block_size=64, bias=True,
+                       act=O.ACT_NONE, seed=100 + M)
+    r = QDenseRun(backend, p)
+    assert r.plan().startswith("qdense_skinny_mfma")
+    check(r, what=f"M={M} w={w_dtype}")
+
+
+@pytest.mark.parametrize("scale_dtype", [O.DT_BFLOAT16, O.DT_FLOAT32])
+@pytest.mark.parametrize("act", range(6))
+def test_skinny_activations_scales(backend, scale_dtype, act):
+    p = O.make_problem(4, 256, 512, w_dtype=O.DT_INT4, scale_dtype=scale_dtype, block_axis=0, block_size=128,
+                       bias=True, act=act, scale_range=(0.01, 0.05), seed=7 * act + scale_dtype)
+    r = QDenseRun(backend, p)
+    assert r.plan() == "qdense_skinny_mfma_i4"
+    check(r, what=f"act {act}")
+
+
+@pytest.mark.parametrize("shape", [(3, 352, 272, 64), (16, 96, 16, 32), (7, 128, 4112, 128), (1, 32, 48, 32),
+                                   (2, 64, 4128, 64)])
+def test_skinny_ragged(backend, shape):
+    """K not a multiple of the group, N not a multiple of 256 columns, single-step K, S = 1.
+    (Packed 4-bit rows are read 32 columns at a time, so N is rounded up to a multiple of 32.)"""
+    M, K, N, G = shape
+    for w_dtype in (O.DT_INT8, O.DT_INT4):
+        if w_dtype == O.DT_INT4:
+            N = (N + 31) // 32 * 32
+        p = O.make_problem(M, K, N, w_dtype=w_dtype, block_axis=0, block_size=G, bias=True, seed=K + N)
+        r = QDenseRun(backend, p)
+        assert r.plan().startswith("qdense_skinny_mfma")
+        check(r, what=f"{shape} {w_dtype}")
+
+
+@pytest.mark.parametrize("w_dtype", [O.DT_INT8, O.DT_INT4])
+def test_skinny_per_channel(backend, w_dtype):
+    """One scale per output column, given as shape [N] (block size = K)."""
+    p = O.make_problem(6, 1024, 512, w_dtype=w_dtype, scale_dtype=O.DT_FLOAT32, block_axis=0, block_size=1024,
+                       per_channel_1d=True, bias=False, seed=3)
+    r = QDenseRun(backend, p)
+    assert r.plan().startswith("qdense_skinny_mfma")
+    check(r, what="per-channel")
+
+
+def test_skinny_c3_config_full_size(backend):
+    """x bf16 [16,4096], int8 [4096,14336] g64 bf16 scales, bias, SiLU."""
+    p = O.baseline_config(2)
+    r = QDenseRun(backend, p)
+    assert r.plan() == "qdense_skinny_mfma_i8"
+    check(r, threads=8, what="C3")
+
+
+def test_skinny_mlp_gate_shape(backend):
+    """The MLP's gate/up projection: x bf16 [8,4096], Int4 [4096,14336] g128 (no activation),
+    and its down projection Int4 [14336,4096] g128."""
+    for K, N in ((4096, 14336), (14336, 4096)):
+        p = O.make_problem(8, K, N, w_dtype=O.DT_INT4, block_axis=0, block_size=128, bias=False,
+                           scale_range=(0.002, 0.02), seed=K)
+        r = QDenseRun(backend, p)
+        assert r.plan() == "qdense_skinny_mfma_i4"
+        check(r, threads=8, what=f"MLP {K}x{N}")
