@@ -193,6 +193,9 @@ int qdense_run(mx_backend* b, const QDenseDesc& d);
 // Skinny-M MFMA kernel (qdense_skinny.hip): shape/layout check and launch.
 bool qdense_skinny_fits(const QDenseDesc& d);
 int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name);
+// Prefill MFMA GEMM (qdense_gemm.hip): shape/layout check and launch.
+bool qdense_gemm_fits(const QDenseDesc& d);
+int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name);
 
 // Normalized DotGeneral: out[b, m, n] = sum_k lhs[b, m, k] * rhs[b, k, n] (or rhs[b, n, k] when
 // rhs_transposed).

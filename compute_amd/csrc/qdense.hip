@@ -306,13 +306,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_dot2_kernel(GemvArgs a) {
 // =============================================================================================
 // Kernel selection.
 // =============================================================================================
-enum class QPath { kEmpty, kExact, kGemvDot2, kSkinny };
+enum class QPath { kEmpty, kExact, kGemvDot2, kSkinny, kGemm };
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 static QPath choose_path(const QDenseDesc& d) {
   if (d.M == 0 || d.N == 0) return QPath::kEmpty;
   if (qdense_skinny_fits(d)) return QPath::kSkinny;
+  if (qdense_gemm_fits(d)) return QPath::kGemm;
   const bool i4 = d.w_dt == MX_DTYPE_INT4 || d.w_dt == MX_DTYPE_UINT4;
   const int64_t cb = i4 ? 256 : 128;
   if (d.M == 1 && d.x_dt == MX_DTYPE_BFLOAT16 && d.scheme == MX_QUANT_LINEAR && !d.zp && d.block_axis == 0 &&
@@ -325,6 +326,8 @@ static QPath choose_path(const QDenseDesc& d) {
 static const char* path_name(const QDenseDesc& d, QPath p) {
   switch (p) {
     case QPath::kEmpty: return "empty";
+    case QPath::kGemm:
+      return d.w_dt == MX_DTYPE_INT8 ? "qdense_gemm_mfma_i8" : "qdense_gemm_mfma_u8";
     case QPath::kSkinny:
       switch (d.w_dt) {
         case MX_DTYPE_INT4: return "qdense_skinny_mfma_i4";
@@ -367,6 +370,8 @@ int qdense_run(mx_backend* b, const QDenseDesc& d) {
       return MX_OK;
     case QPath::kSkinny:
       return qdense_skinny_run(b, d, name);
+    case QPath::kGemm:
+      return qdense_gemm_run(b, d, name);
     case QPath::kGemvDot2: {
       const bool i4 = d.w_dt == MX_DTYPE_INT4 || d.w_dt == MX_DTYPE_UINT4;
       const int cbw = i4 ? 256 : 128;

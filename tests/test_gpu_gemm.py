@@ -1,0 +1,60 @@
+"""Prefill FusedQuantizedDense (M > 16 bf16 rows, int8/uint8 weights, one scale per output
+column): the dequantise-into-MFMA GEMM on the GPU vs the CPU oracle.
+
+The kernel factors the per-channel scale out of the K sum and accumulates in f32 on the matrix
+cores in another order than the reference loop, so: bf16 outputs within rel 1e-2 / abs 1e-3 of
+the oracle's f32 result, and (without activation) within 2^-8 relative (bf16 rounding) plus
+1e-5 of sum|terms| of the exact f64 value.  Large cases check a seeded sample of rows (the
+oracle computes rows independently).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.qd_helpers import QDenseRun, assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+
+
+def check_rows(r: QDenseRun, rows=None, threads=1, what=""):
+    p = r.p
+    y = r.run()
+    sel = slice(None) if rows is None else rows
+    assert_bf16_close(y[sel], O.qdense_f32(p, rows=rows, threads=threads), what=what)
+    if p.act == O.ACT_NONE:
+        truth = O.qdense_f64(p, rows)
+        scale = O.qdense_f64(p, rows, absolute=True)
+        got = O.bf16_to_f32(y[sel]).astype(np.float64)
+        assert np.all(np.abs(got - truth) <= 2.0 ** -8 * np.abs(truth) + 1e-5 * scale), what
+    return y
+
+
+@pytest.mark.parametrize("shape", [(17, 64, 16), (300, 128, 272), (512, 256, 384), (256, 640, 128), (1000, 64, 4112)])
+@pytest.mark.parametrize("w_dtype", [O.DT_INT8, O.DT_UINT8])
+def test_gemm_shapes(backend, shape, w_dtype):
+    M, K, N = shape
+    p = O.make_problem(M, K, N, w_dtype=w_dtype, block_axis=0, block_size=K, per_channel_1d=True,
+                       scale_dtype=O.DT_FLOAT32, bias=True, seed=M + K + N)
+    r = QDenseRun(backend, p)
+    assert r.plan().startswith("qdense_gemm_mfma")
+    check_rows(r, what=f"{shape}")
+
+
+@pytest.mark.parametrize("act", range(6))
+def test_gemm_activations(backend, act):
+    p = O.make_problem(64, 128, 256, w_dtype=O.DT_INT8, block_axis=0, block_size=128, per_channel_1d=True,
+                       scale_dtype=O.DT_BFLOAT16, bias=True, act=act, scale_range=(0.01, 0.05), seed=act)
+    r = QDenseRun(backend, p)
+    assert r.plan() == "qdense_gemm_mfma_i8"
+    check_rows(r, what=f"act {act}")
+
+
+def test_gemm_c4_config_full_size(backend):
+    """x bf16 [2048,4096], int8 [4096,4096] per-channel f32 scales, bias,
+    exact GELU.  128 seeded rows are checked against the oracle; two calls must agree bitwise."""
+    p = O.baseline_config(3)
+    r = QDenseRun(backend, p)
+    assert r.plan() == "qdense_gemm_mfma_i8"
+    rows = np.sort(np.random.default_rng(4).choice(p.M, 128, replace=False))
+    y = check_rows(r, rows=rows, threads=8, what="C4")
+    assert np.array_equal(y, r.run())
