@@ -7,11 +7,17 @@ no bias.  A step is one Execute of the compiled graph over one batch, with every
 resident in HBM.  Weight sets are rotated (> 512 MB of distinct copies) so each step reads its
 weights from HBM rather than the 256 MB Infinity Cache.
 
-Output: one JSON line (see `--help`).  `value` is algorithmic bytes per step / wall time per
-step over K back-to-back steps (host launch overhead included); `roofline` prices the dominant
-kernel's average duration from HIP events on the backend's stream; `cpu_baseline` times the
-CPU restatement of the reference loop (oracle/, the reference itself is Go and cannot be built
-here) on a bounded sample on this host.
+The JSON line also reports, under "extra", the other BASELINE configurations measured the same
+way: C3 batched decode (HBM roofline), C4 prefill (bf16 MFMA roofline) and C5, the quantized MLP
+graph built through the Builder API (microseconds per Execute, 100 resident calls).
+
+`value` is algorithmic bytes per step / wall time per step over K back-to-back steps (host
+launch overhead included).  `roofline` prices the dominant kernel's average duration, taken from
+HIP events recorded on the backend's stream around every launch over the same K steps.
+`traffic` (HBM bytes per launch) is read from profiles/traffic.json, which is produced from
+rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this script (see --copy-calibration).
+`cpu_baseline` times the CPU restatement of the reference loop (oracle/, the reference itself is
+Go and cannot be built here) on a bounded sample on this host.
 """
 from __future__ import annotations
 
@@ -28,9 +34,12 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
+METRIC = "QuantizedDense GB/s & TFLOP/s vs MI355X roofline; µs/call at decode+prefill"
 
 
 def measure(backend, wl, steps: int, warmup: int, rotate_bytes: int = 2 * MALL_BYTES):
+    """Wall time per step over `steps` back-to-back Executes, then the same steps again with a
+    HIP event pair around every kernel launch (per-kernel average durations)."""
     exe = wl.compile(backend)
     n_sets = max(1, math.ceil(rotate_bytes / max(1, wl.weight_bytes())))
     n_sets = min(n_sets, 64)
@@ -38,12 +47,10 @@ def measure(backend, wl, steps: int, warmup: int, rotate_bytes: int = 2 * MALL_B
     backend.SetProfiling(False)
     exe.ExecuteLoop(sets, warmup)
     backend.Synchronize()
-    # Timed region: K back-to-back steps (no per-step host sync), then one sync.
     t0 = time.perf_counter()
     exe.ExecuteLoop(sets, steps)
     backend.Synchronize()
     wall = time.perf_counter() - t0
-    # Same K steps with a HIP event pair around every kernel launch (the kernel durations).
     backend.SetProfiling(True)
     backend.ProfileReset()
     exe.ExecuteLoop(sets, steps)
@@ -54,15 +61,35 @@ def measure(backend, wl, steps: int, warmup: int, rotate_bytes: int = 2 * MALL_B
         for b in s:
             b.Finalize()
     exe.Finalize()
-    kname, (launches, total_ms) = max(prof.items(), key=lambda kv: kv[1][1])
-    return {
-        "ms_per_step": wall / steps * 1e3,
-        "kernel": kname,
-        "kernel_us": total_ms / launches * 1e3,
-        "kernel_launches_per_step": launches / steps,
-        "profile": {k: {"launches": v[0], "avg_us": v[1] / v[0] * 1e3} for k, v in prof.items()},
-        "weight_sets": n_sets,
-    }
+    kernels = {k: {"launches_per_step": v[0] / steps, "avg_us": v[1] / v[0] * 1e3} for k, v in prof.items()}
+    kname = max(prof.items(), key=lambda kv: kv[1][1])[0]
+    kernel_us_per_step = sum(v[1] for v in prof.values()) / steps * 1e3
+    return {"ms_per_step": wall / steps * 1e3, "kernel": kname, "kernel_us": kernels[kname]["avg_us"],
+            "kernels": kernels, "kernel_us_per_step": kernel_us_per_step, "weight_sets": n_sets}
+
+
+def traffic_for(name: str):
+    """HBM bytes per launch of the workload's dominant kernel from profiles/traffic.json."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        v = t.get(name)
+        return None if v is None else int(v["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError, TypeError):
+        return None
+
+
+def hbm_roofline(nbytes: float, us: float, traffic):
+    achieved = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+
+
+def mfma_roofline(flops: float, us: float, traffic):
+    achieved = flops / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic}
 
 
 def cpu_baseline(wl, seconds: float):
@@ -90,31 +117,77 @@ def cpu_baseline(wl, seconds: float):
             "sample": f"{calls} full calls of {wl.name} in {el:.1f} s ({el / calls * 1e3:.2f} ms/call)"}
 
 
+def copy_calibration(mib: int, iters: int):
+    """A plain device-to-device copy of known size (for scaling the FETCH_SIZE / WRITE_SIZE
+    counters to bytes): `iters` copies of `mib` MiB."""
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": n, "launches": iters}), flush=True)
+
+
+def extra_entry(wl, r):
+    nbytes = wl.algorithmic_bytes()
+    e = {"us_per_call": round(r["ms_per_step"] * 1e3, 2), "kernel": r["kernel"], "kernel_us": round(r["kernel_us"], 3),
+         "kernel_us_per_call": round(r["kernel_us_per_step"], 3)}
+    if wl.name.startswith("C4"):
+        e["TFLOPs_kernel"] = round(wl.flops() / (r["kernel_us"] * 1e-6) / 1e12, 1)
+        e["roofline"] = mfma_roofline(wl.flops(), r["kernel_us"], traffic_for(wl.name))
+    elif wl.name.startswith("C5"):
+        # Whole graph per call: the three quantized projections dominate; price all kernels of one
+        # call against HBM.
+        e["GBps_call"] = round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1)
+        e["kernels"] = {k: {"per_call": round(v["launches_per_step"], 2), "avg_us": round(v["avg_us"], 3)}
+                        for k, v in r["kernels"].items()}
+        e["roofline"] = hbm_roofline(nbytes, r["kernel_us_per_step"], traffic_for(wl.name))
+    else:
+        e["GBps_kernel"] = round(nbytes / (r["kernel_us"] * 1e-6) / 1e9, 1)
+        e["roofline"] = hbm_roofline(nbytes, r["kernel_us"], traffic_for(wl.name))
+    return e
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--extra", default="C1,C3", help="comma list of other configs to report under 'extra'")
+    ap.add_argument("--extra", default="C3,C4,C5", help="comma list of other configs to report under 'extra'")
+    ap.add_argument("--only", default="", help="run only this config (profiling passes); prints its entry")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one MI355X; --gpus {args.gpus} is not supported "
               "(the quantized-dense path shards by output columns with no collective on one GPU)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration, 20)
+        return
 
     import compute_amd as ca
     from compute_amd import workloads
 
     backend = ca.New("mi355x")
+    if args.only:
+        wl = workloads.make(args.only)
+        r = measure(backend, wl, args.steps, args.warmup)
+        print(json.dumps({"workload": wl.name, **extra_entry(wl, r)}), flush=True)
+        backend.Finalize()
+        return
+
     wl = workloads.make("C2")
     r = measure(backend, wl, args.steps, args.warmup)
     nbytes = wl.algorithmic_bytes()
     value = nbytes / (r["ms_per_step"] * 1e-3) / 1e9
-    achieved = nbytes / (r["kernel_us"] * 1e-6) / 1e9
     out = {
-        "metric": "QuantizedDense GB/s & TFLOP/s vs MI355X roofline; us/call at decode+prefill",
+        "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -124,28 +197,20 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "int4 weights, bf16 activations, f32 accumulate",
         "data": "synthetic (seeded; weights rotated over %d distinct HBM copies)" % r["weight_sets"],
         "config": {"workload": wl.name, "M": wl.M, "K": wl.K, "N": wl.N, "weights": "Int4 reference packing",
                    "group_size": wl.block_size, "scales": "bf16 [32,11008]", "bias": None, "activation": "none",
                    "algorithmic_bytes": nbytes, "us_per_call": round(r["ms_per_step"] * 1e3, 2),
                    "kernel_us": round(r["kernel_us"], 3), "kernel": r["kernel"],
                    "tflops": round(wl.flops() / (r["ms_per_step"] * 1e-3) / 1e12, 3)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "roofline": hbm_roofline(nbytes, r["kernel_us"], traffic_for(wl.name)),
     }
     extra = {}
     for name in [n for n in args.extra.split(",") if n]:
         w2 = workloads.make(name)
-        steps = max(3, min(args.steps, 50))
-        r2 = measure(backend, w2, steps, 2)
-        b2 = w2.algorithmic_bytes()
-        extra[w2.name] = {
-            "us_per_call": round(r2["ms_per_step"] * 1e3, 2), "kernel": r2["kernel"],
-            "kernel_us": round(r2["kernel_us"], 3),
-            "GBps_kernel": round(b2 / (r2["kernel_us"] * 1e-6) / 1e9, 1),
-            "TFLOPs_kernel": round(w2.flops() / (r2["kernel_us"] * 1e-6) / 1e12, 3),
-        }
+        steps = 100 if name == "C5" else max(3, min(args.steps, 50))
+        extra[w2.name] = extra_entry(w2, measure(backend, w2, steps, 5))
     if extra:
         out["extra"] = extra
     if not args.no_cpu_baseline:

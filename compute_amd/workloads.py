@@ -72,12 +72,75 @@ class QDWorkload:
         return 2 * self.M * self.K * self.N
 
 
+@dataclass
+class MLPWorkload:
+    """the quantized MLP built through the Builder API, batch 8 x seq 1:
+    RMSNorm (eps 1e-6, no gamma) over bf16 x [8,4096]; gate and up FusedQuantizedDense Int4 g128
+    [4096 -> 14336] (SiLU fused into gate's epilogue); SiLU(gate) * up; down FusedQuantizedDense
+    Int4 g128 [14336 -> 4096]; residual add.  RMSNorm runs in f32 (ConvertDType around it)."""
+
+    name: str
+    M: int
+    D: int
+    F: int
+    G: int
+    x: np.ndarray
+    weights: list  # [(w packed, scale bf16 bits, K, N)] for gate, up, down
+    eps: float = 1e-6
+
+    def shapes(self):
+        s = [Shape(BFloat16, self.M, self.D)]
+        for w, sc, K, N in self.weights:
+            s += [Shape(Int4, K, N), Shape(BFloat16, K // self.G, N)]
+        return s
+
+    def host_inputs(self):
+        d = [self.x]
+        for w, sc, _, _ in self.weights:
+            d += [w, sc]
+        return d
+
+    def compile(self, backend: B.Backend) -> B.Executable:
+        bld = backend.Builder(self.name)
+        f = bld.Main()
+        names = ["x", "w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down"]
+        p = [f.Parameter(n, sh) for n, sh in zip(names, self.shapes())]
+        x = p[0]
+        xf = f.ConvertDType(x, Float32)
+        ms = f.Mul(f.ReduceSum(f.Mul(xf, xf), 1), f.Constant(np.full(self.M, 1.0 / self.D, np.float32)))
+        inv = f.Rsqrt(f.Add(ms, f.Constant(np.full(self.M, self.eps, np.float32))))
+        h = f.ConvertDType(f.Mul(xf, f.BroadcastInDim(inv, Shape(Float32, self.M, self.D), [0])), BFloat16)
+
+        def qd(v, w, sc, act):
+            q = B.Quantization(B.QuantLinear, sc, None, 0, self.G)
+            return f.FusedQuantizedDense(v, w, None, q, B.ActivationType(act))
+
+        g = qd(h, p[1], p[2], B.ActivationSilu)
+        u = qd(h, p[3], p[4], B.ActivationNone)
+        d = qd(f.Mul(g, u), p[5], p[6], B.ActivationNone)
+        f.Return([f.Add(d, x)])
+        return bld.Compile()
+
+    def upload(self, backend: B.Backend):
+        return [backend.BufferFromFlatData(0, d.ravel(), s) for d, s in zip(self.host_inputs(), self.shapes())]
+
+    def weight_bytes(self) -> int:
+        return sum(w.nbytes for w, _, _, _ in self.weights)
+
+    def algorithmic_bytes(self) -> int:
+        """Weights and scales read once, x read once, the output written once."""
+        return sum(a.nbytes for a in self.host_inputs()) + self.M * self.D * 2
+
+    def flops(self) -> int:
+        return sum(2 * self.M * K * N for _, _, K, N in self.weights)
+
+
 def _rngs(seed: int, n: int):
     return [np.random.Generator(np.random.PCG64(s)) for s in np.random.SeedSequence(seed).spawn(n)]
 
 
 def make(name: str, seed: int = 0) -> QDWorkload:
-    """C1 .. C4."""
+    """C1 .. C5."""
     rx, rw, rs, rb = _rngs(seed, 4)
     if name == "C1":  # int8 per-channel, x f32 [4,512] U(-1,1), bias f32, no activation
         M, K, N = 4, 512, 512
@@ -110,4 +173,13 @@ def make(name: str, seed: int = 0) -> QDWorkload:
         b = bf16_from_f32((rb.standard_normal(N) * 0.02).astype(np.float32))
         return QDWorkload("C4_prefill_int8_perchannel_gelu", M, K, N, BFloat16, Int8, Float32, (N,), 0, K, BFloat16,
                           B.ActivationGelu, x, w, s, b)
+    if name == "C5":  # quantized MLP graph, batch 8, Int4 g128, scales U(0.002, 0.02)
+        M, D, F, G = 8, 4096, 14336, 128
+        x = bf16_from_f32(rx.standard_normal((M, D)).astype(np.float32))
+        ws = []
+        for K, N in ((D, F), (D, F), (F, D)):
+            w = pack_int4(rw.integers(-8, 8, K * N))
+            sc = bf16_from_f32(rs.uniform(0.002, 0.02, (K // G, N)).astype(np.float32))
+            ws.append((w, sc, K, N))
+        return MLPWorkload("C5_mlp_int4_g128_batch8", M, D, F, G, x, ws)
     raise ValueError(f"unknown workload {name}")
