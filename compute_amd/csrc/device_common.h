@@ -150,29 +150,4 @@ __device__ __forceinline__ float act_fast(float x, int act) {
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Split-K completion: every workgroup that owns one K slice of a tile calls this after storing
-// its partial results; it returns true (in all threads) only in the workgroup that arrives
-// last, which may then read every slice's partials and finish the tile.
-//
-// Cost matters here: an agent-scope fence on gfx950 writes back (release) or invalidates
-// (acquire) the whole L2 of the XCD.  So the workgroup barrier first orders the other waves'
-// stores before thread 0's single release RMW, and only the last arriver acquires.  The counter
-// is reset for the next launch by the last arriver (no other workgroup touches it afterwards).
-// ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ bool splitk_last_arriver(uint32_t* counter, uint32_t arrivals, int* s_flag) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == arrivals - 1u;
-    if (last) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    *s_flag = last;
-  }
-  __syncthreads();
-  return *s_flag != 0;
-}
-
 }  // namespace mx

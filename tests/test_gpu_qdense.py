@@ -17,7 +17,7 @@ from tests.qd_helpers import QDenseRun, assert_bf16_close, run_qdense
 pytestmark = pytest.mark.gpu
 
 W_DTYPES = [O.DT_INT8, O.DT_UINT8, O.DT_INT4, O.DT_UINT4]
-FAST_DECODE = ("qdense_gemv_dot2", "qdense_skinny_mfma")
+FAST_DECODE = "qdense_skinny_mfma"
 
 
 # ---------------------------------------------------------------------------------------------
@@ -79,7 +79,7 @@ def test_empty_and_zero_k(backend):
 
 
 # ---------------------------------------------------------------------------------------------
-# Decode GEMV (M = 1, bf16).
+# Decode (M = 1, bf16): the skinny MFMA kernel.
 # ---------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("w_dtype", W_DTYPES)
 @pytest.mark.parametrize("scale_dtype", [O.DT_BFLOAT16, O.DT_FLOAT32])
