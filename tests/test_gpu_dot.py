@@ -1,0 +1,179 @@
+"""DotGeneral and FusedDense on the GPU (the contraction FusedQuantizedDense lowers onto),
+mirroring the reference's compliance cases (support/backendtest/dotgeneral.go, fusedops.go):
+known answers from tests/golden/reference_kats.json, the dtype matrix, the TransposedLarge
+brute force with the reference's own tolerance (abs 0.5 or rel 3%), and seeded random batched /
+transposed layouts against the f64 restatement (oracle.dot_general)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import compute_amd as ca
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
+
+
+def run(backend, inputs, build):
+    """inputs: [(numpy storage array, DType)]; build(f, params) -> Value.  Returns the output."""
+    bld = backend.Builder("dot")
+    f = bld.Main()
+    params = [f.Parameter(f"p{i}", ca.Shape(dt, *a.shape)) for i, (a, dt) in enumerate(inputs)]
+    f.Return([build(f, params)])
+    exe = bld.Compile()
+    bufs = [backend.BufferFromFlatData(0, a.ravel(), ca.Shape(dt, *a.shape)) for a, dt in inputs]
+    out = exe.Execute(bufs)[0]
+    sh = out.Shape()
+    return out.ToFlatData().reshape(sh.dimensions), sh.dtype
+
+
+def test_shuffled_axes_kat(backend):
+    k = GOLDEN["dot_general_shuffled_axes"]
+    lhs = np.arange(1, 1 + np.prod(k["lhs_iota_from_1_shape"]), dtype=np.float32).reshape(k["lhs_iota_from_1_shape"])
+    rhs = np.arange(1, 1 + np.prod(k["rhs_iota_from_1_shape"]), dtype=np.float32).reshape(k["rhs_iota_from_1_shape"])
+    y, _ = run(backend, [(lhs, ca.Float32), (rhs, ca.Float32)],
+               lambda f, p: f.DotGeneral(p[0], k["lhs_contracting"], k["lhs_batch"], p[1], k["rhs_contracting"],
+                                         k["rhs_batch"]))
+    assert np.array_equal(y, np.array(k["want"], np.float32))
+
+
+def test_axis_transposition_kat(backend):
+    k = GOLDEN["dot_general_axis_transposition"]
+    y, _ = run(backend, [(np.array(k["lhs"], np.float32), ca.Float32), (np.array(k["rhs"], np.float32), ca.Float32)],
+               lambda f, p: f.DotGeneral(p[0], k["lhs_contracting"], k["lhs_batch"], p[1], k["rhs_contracting"],
+                                         k["rhs_batch"]))
+    assert np.array_equal(y, np.array(k["want"], np.float32))
+
+
+def test_f64_very_large_kat(backend):
+    k = GOLDEN["dot_general_f64_very_large"]
+    lhs = ((np.arange(np.prod(k["lhs_shape"])) + 1.0) * 1e-5).reshape(k["lhs_shape"])
+    rhs = np.ones(k["rhs_shape"])
+    y, dt = run(backend, [(lhs, ca.Float64), (rhs, ca.Float64)], lambda f, p: f.DotGeneral(p[0], [2], [], p[1], [0], []))
+    assert dt == ca.Float64 and abs(y[0, 0, 0] - k["want_out_0_0_0"]) < k["tolerance"]
+    assert np.allclose(y, O.dot_general(lhs, [2], [], rhs, [0], []), rtol=1e-12, atol=0)
+
+
+def test_bf16_f32_accumulation_kat(backend):
+    k = GOLDEN["dot_general_bf16_f32_acc"]
+    lhs = O.bf16_round(np.array(k["lhs"], np.float32))
+    rhs = O.bf16_round(np.array(k["rhs"], np.float32))
+    y, dt = run(backend, [(lhs, ca.BFloat16), (rhs, ca.BFloat16)],
+                lambda f, p: f.DotGeneral(p[0], [1], [], p[1], [0], [], ca.DotGeneralConfig(AccumulatorDType=ca.Float32)))
+    assert dt == ca.BFloat16 and O.bf16_to_f32(y)[0, 0] == k["want"]
+
+
+def test_small_matmul_kats(backend):
+    k = GOLDEN["dot_general_small_matmul"]
+    a, b = np.array(k["a"], np.float32), np.array(k["b"], np.float32)
+    for rc, want in (([0], k["non_transposed"]), ([1], k["transposed"])):
+        y, _ = run(backend, [(a, ca.Float32), (b, ca.Float32)], lambda f, p: f.DotGeneral(p[0], [1], [], p[1], rc, []))
+        assert np.array_equal(y, np.array(want, np.float32))
+    vec, mat, mat2 = (np.array(k[n], np.float32) for n in ("vec", "mat", "mat2"))
+    y, _ = run(backend, [(vec, ca.Float32), (mat, ca.Float32)], lambda f, p: f.DotGeneral(p[0], [0], [], p[1], [0], []))
+    assert np.array_equal(y, np.array(k["vec_mat"], np.float32))
+    y, _ = run(backend, [(mat2, ca.Float32), (vec, ca.Float32)], lambda f, p: f.DotGeneral(p[0], [1], [], p[1], [0], []))
+    assert np.array_equal(y, np.array(k["mat_vec"], np.float32))
+
+
+def test_dot_product_kats(backend):
+    k = GOLDEN["dot_general_dot"]
+    x, yv, x2 = (np.array(k[n], np.float32) for n in ("x", "y", "x2"))
+    y, _ = run(backend, [(x, ca.Float32), (yv, ca.Float32)], lambda f, p: f.DotGeneral(p[0], [0], [], p[1], [0], []))
+    assert float(y) == k["want"]
+    y, _ = run(backend, [(x2, ca.Float32), (yv, ca.Float32)], lambda f, p: f.DotGeneral(p[0], [1], [], p[1], [0], []))
+    assert np.array_equal(y, np.array(k["want2"], np.float32))
+
+
+FLOATS = [ca.Float16, ca.BFloat16, ca.Float32, ca.Float64]
+
+
+@pytest.mark.parametrize("in_dt", FLOATS)
+@pytest.mark.parametrize("acc_dt", [ca.InvalidDType] + FLOATS)
+@pytest.mark.parametrize("out_dt", [ca.InvalidDType] + FLOATS)
+def test_dtype_matrix(backend, in_dt, acc_dt, out_dt):
+    """dotgeneral.go:444-497: iota(16) . iota(16) = 1240 for every input/accumulator/output dtype;
+    the output dtype is OutputDType, or the input dtype when unset."""
+    def build(f, _):
+        lhs = f.Iota(ca.Shape(in_dt, 16), 0)
+        rhs = f.Iota(ca.Shape(in_dt, 16), 0)
+        return f.DotGeneral(lhs, [0], [], rhs, [0], [], ca.DotGeneralConfig(AccumulatorDType=acc_dt, OutputDType=out_dt))
+
+    try:
+        y, dt = run(backend, [], build)
+    except ca.ErrNotImplemented as e:
+        pytest.skip(f"combination not implemented: {e}")
+    want_dt = out_dt if out_dt != ca.InvalidDType else in_dt
+    assert dt == want_dt
+    v = float(O.bf16_to_f32(y)) if dt == ca.BFloat16 else float(y)
+    assert v == 1240.0
+
+
+def test_transposed_large(backend):
+    """dotgeneral.go:499-599, same data and tolerance (abs 0.5 or rel 3%)."""
+    lhs = (np.arange(4 * 32 * 8 * 2, dtype=np.float64) * 1e-4).astype(np.float32)
+    lhs = np.repeat(lhs, 256).reshape(4, 32, 8, 2, 256)
+    rhs = (np.arange(4 * 32 * 8 * 256, dtype=np.float64) * 1e-4).astype(np.float32).reshape(4, 32, 8, 256)
+    y, _ = run(backend, [(lhs, ca.Float32), (rhs, ca.Float32)],
+               lambda f, p: f.DotGeneral(p[0], [4], [0, 2], p[1], [3], [0, 2]))
+    want = O.dot_general(lhs.astype(np.float64), [4], [0, 2], rhs.astype(np.float64), [3], [0, 2]).astype(np.float32)
+    assert y.shape == want.shape == (4, 8, 32, 2, 32)
+    diff = np.abs(y - want)
+    assert np.all((diff <= 0.5) | (diff / np.maximum(np.abs(want), 1e-30) < 0.03))
+
+
+@pytest.mark.parametrize("dt", [ca.Float32, ca.BFloat16, ca.Float16])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_random_batched(backend, dt, transposed):
+    """[B, M, K] x [B, K, N] (or [B, N, K]) with random data vs the f64 restatement: f32 within
+    1e-5 of sum|terms|; half precision (f32 accumulation, rounded output) within rel 1e-2 /
+    abs 1e-3 of the f64 value."""
+    rng = np.random.default_rng(int(dt) + 7 * transposed)
+    B, M, K, N = 3, 70, 130, 90
+    lf = rng.standard_normal((B, M, K)).astype(np.float32)
+    rf = rng.standard_normal((B, N, K) if transposed else (B, K, N)).astype(np.float32)
+    if dt == ca.BFloat16:
+        lhs, rhs = O.bf16_round(lf), O.bf16_round(rf)
+        lv, rv = O.bf16_to_f32(lhs), O.bf16_to_f32(rhs)
+    elif dt == ca.Float16:
+        lhs, rhs = lf.astype(np.float16), rf.astype(np.float16)
+        lv, rv = lhs.astype(np.float32), rhs.astype(np.float32)
+    else:
+        lhs, rhs, lv, rv = lf, rf, lf, rf
+    rc = [2] if transposed else [1]
+    y, odt = run(backend, [(lhs, dt), (rhs, dt)], lambda f, p: f.DotGeneral(p[0], [2], [0], p[1], rc, [0]))
+    assert odt == dt
+    truth = O.dot_general(lv.astype(np.float64), [2], [0], rv.astype(np.float64), rc, [0])
+    got = O.bf16_to_f32(y) if dt == ca.BFloat16 else y.astype(np.float32)
+    if dt == ca.Float32:
+        scale = O.dot_general(np.abs(lv).astype(np.float64), [2], [0], np.abs(rv).astype(np.float64), rc, [0])
+        assert np.all(np.abs(got - truth) <= 1e-5 * scale)
+    else:
+        assert np.all(np.abs(got - truth) <= 1e-3 + 1e-2 * np.abs(truth))
+
+
+@pytest.mark.parametrize("case", ["fused_dense_none", "fused_dense_relu"])
+def test_fused_dense_kats(backend, case):
+    k = GOLDEN[case]
+    act = ca.ActivationNone if case.endswith("none") else ca.ActivationRelu
+    x, w, b = (np.array(k[n], np.float32) for n in ("x", "w", "bias"))
+    y, _ = run(backend, [(x, ca.Float32), (w, ca.Float32), (b, ca.Float32)],
+               lambda f, p: f.FusedDense(p[0], p[1], p[2], act))
+    assert np.array_equal(y, np.array(k["want"], np.float32))
+
+
+@pytest.mark.parametrize("act", range(6))
+def test_fused_dense_random(backend, act):
+    rng = np.random.default_rng(act)
+    x = rng.standard_normal((33, 100)).astype(np.float32)
+    w = (rng.standard_normal((100, 50)) * 0.1).astype(np.float32)
+    b = (rng.standard_normal(50) * 0.1).astype(np.float32)
+    y, _ = run(backend, [(x, ca.Float32), (w, ca.Float32), (b, ca.Float32)],
+               lambda f, p: f.FusedDense(p[0], p[1], p[2], ca.ActivationType(act)))
+    pre = x.astype(np.float64) @ w.astype(np.float64) + b
+    want = O.act(pre.astype(np.float32), act)
+    scale = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64) + np.abs(b)
+    assert np.all(np.abs(y - want) <= 1e-5 * scale + 1e-6)
