@@ -6,20 +6,23 @@
 // s[n] the reference's terms (x*w)*s factor as  y[m,n] = act(bias[n] + s[n] * sum_k x[m,k]*w[k,n]);
 // every product x*w is exact in f32, so only the summation order differs from the reference.
 //
-// Tiling.  A workgroup (4 waves) computes a 256 x 128 output tile; wave w owns rows
-// [64w, 64w+64) x all 128 columns.  K advances in blocks of 64 through a 3-stage LDS ring that
-// is filled by direct global->LDS loads (16 bytes per lane, issued two blocks ahead):
+// Tiling.  A workgroup (8 waves, two per SIMD) computes a 256 x 128 output tile; wave w owns
+// rows [64 wr, 64 wr + 64) x columns [64 wc, 64 wc + 64) with wr = w % 4, wc = w / 4.  K advances
+// in blocks of 64 through a 3-stage LDS ring filled by direct global->LDS loads (16 bytes per
+// lane, issued two blocks ahead):
 //   - x tile [256 rows][64 k] bf16 (32 KB), its 16-byte chunks XOR-swizzled within each row by
 //     (row >> 1) & 7 so that the 16 rows of an MFMA operand read land in distinct LDS banks;
-//   - w tile [64 k][128 columns] int8 (8 KB), stored as 8 blocks of 8 rows with a 128-byte gap
-//     between blocks so that the two row groups read together use different banks.
+//   - w tile [64 k][128 columns] int8 (8 KB), stored as 8 blocks of 8 rows with a 64-byte gap
+//     between blocks so that the four row groups read together use different banks.
 // Per 32-row K step a wave reads its 4 row blocks of x as the A operands of
-// v_mfma_f32_16x16x32_bf16 and, for B, 8 rows x 8 columns of int8 per lane, converted exactly to
-// bf16 pairs (|w| < 256 has at most 8 significant bits) in registers: 8 B operands (column c of
-// every lane's 8 columns), so 32 MFMAs per step share each converted operand 4 times.
-// Lane (cg = lane % 16, kq = lane / 16) ends with rows 4*kq + r of each 16-row block and the
-// 8 consecutive columns 8*cg .. 8*cg + 7; the epilogue applies scale, bias and activation and
-// writes 16-byte bf16 rows.
+// v_mfma_f32_16x16x32_bf16 and, for B, 8 rows x 4 columns of int8 per lane, converted exactly to
+// bf16 pairs (|w| < 256 has at most 8 significant bits) in registers: 4 B operands (column c of
+// every lane's 4 columns), 16 MFMAs per step.  With two waves per SIMD one wave's conversion
+// overlaps the other's MFMAs.  Lane (cg = lane % 16, kq = lane / 16) ends with rows 4*kq + r of
+// each 16-row block and the 4 consecutive columns 4*cg .. 4*cg + 3 of its wave's 64; the
+// epilogue applies scale, bias and activation and writes 8-byte bf16 runs.
+// Tile order: every XCD (workgroups are dispatched round-robin over the 8) takes a 2 x 16 block
+// of tiles, so its L2 serves the x rows and w columns they share.
 #include <algorithm>
 
 #include "device_common.h"
@@ -35,15 +38,16 @@ typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 typedef __attribute__((address_space(1))) void* gbl_void_ptr;
 
-constexpr int kBM = 256, kBN = 128, kBK = 64, kThreads = 256, kStages = 3;
-constexpr int kABytes = kBM * kBK * 2;         // 32 KB
-constexpr int kBPitch = 8 * kBN + 128;         // one 8-row block of w plus the bank gap
-constexpr int kBBytes = (kBK / 8) * kBPitch;   // 9 KB
+constexpr int kBM = 256, kBN = 128, kBK = 64, kWaves = 8, kThreads = 64 * kWaves, kStages = 3;
+constexpr int kABytes = kBM * kBK * 2;              // 32 KB
+constexpr int kBPitch = 8 * kBN + 64;               // one 8-row block of w plus the bank gap
+constexpr int kBBytes = (kBK / 8) * kBPitch;        // 8.5 KB
 constexpr int kStage = kABytes + kBBytes;
 constexpr int kLds = kStages * kStage;
-constexpr int kAInstr = kABytes / (4 * 1024);  // DMA loads per wave per stage (x)
-constexpr int kBInstr = (kBK / 8) / 4;         // DMA loads per wave per stage (w)
+constexpr int kAInstr = kABytes / (kWaves * 1024);  // DMA loads per wave per stage (x)
+constexpr int kBInstr = (kBK / 8) / kWaves;         // DMA loads per wave per stage (w)
 constexpr int kP = kAInstr + kBInstr;
+static_assert(kAInstr * kWaves * 1024 == kABytes && kBInstr * kWaves == kBK / 8, "DMA split");
 
 struct GemmArgs {
   const uint16_t* x;  // [M, K] bf16
@@ -51,7 +55,7 @@ struct GemmArgs {
   const void* scale;  // [N]
   const void* bias;   // [N] or null
   uint16_t* out;      // [M, N] bf16
-  int M, K, N, s_dt, b_dt, act, tiles_n;
+  int M, K, N, s_dt, b_dt, act, tiles_n, grouped;
 };
 
 __device__ __forceinline__ void dma16(const void* src, void* lds) {
@@ -74,22 +78,22 @@ __device__ __forceinline__ f32x4_t mfma(const u32x4_v& a, const u32x4_v& b, f32x
 }
 
 // One K step's operands from LDS: the wave's 4 x-row blocks (16 bytes each, blocks 2 KB apart)
-// and 8 rows x 8 bytes of w.  One asm block completes them together: ordinary LDS reads after
+// and 8 rows x 4 bytes of w.  One asm block completes them together: ordinary LDS reads after
 // LDS-DMA loads would make the compiler wait for every outstanding DMA.
-__device__ __forceinline__ void read_step(uint32_t aa, uint32_t ba, u32x4_v (&A)[4], u32x2_v (&B)[8]) {
+__device__ __forceinline__ void read_step(uint32_t aa, uint32_t ba, u32x4_v (&A)[4], uint32_t (&B)[8]) {
   asm volatile(
       "ds_read_b128 %0, %12 offset:0\n\t"
       "ds_read_b128 %1, %12 offset:2048\n\t"
       "ds_read_b128 %2, %12 offset:4096\n\t"
       "ds_read_b128 %3, %12 offset:6144\n\t"
-      "ds_read_b64 %4, %13 offset:0\n\t"
-      "ds_read_b64 %5, %13 offset:128\n\t"
-      "ds_read_b64 %6, %13 offset:256\n\t"
-      "ds_read_b64 %7, %13 offset:384\n\t"
-      "ds_read_b64 %8, %13 offset:512\n\t"
-      "ds_read_b64 %9, %13 offset:640\n\t"
-      "ds_read_b64 %10, %13 offset:768\n\t"
-      "ds_read_b64 %11, %13 offset:896\n\t"
+      "ds_read_b32 %4, %13 offset:0\n\t"
+      "ds_read_b32 %5, %13 offset:128\n\t"
+      "ds_read_b32 %6, %13 offset:256\n\t"
+      "ds_read_b32 %7, %13 offset:384\n\t"
+      "ds_read_b32 %8, %13 offset:512\n\t"
+      "ds_read_b32 %9, %13 offset:640\n\t"
+      "ds_read_b32 %10, %13 offset:768\n\t"
+      "ds_read_b32 %11, %13 offset:896\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(A[0]), "=&v"(A[1]), "=&v"(A[2]), "=&v"(A[3]), "=&v"(B[0]), "=&v"(B[1]), "=&v"(B[2]), "=&v"(B[3]),
         "=&v"(B[4]), "=&v"(B[5]), "=&v"(B[6]), "=&v"(B[7])
@@ -97,37 +101,46 @@ __device__ __forceinline__ void read_step(uint32_t aa, uint32_t ba, u32x4_v (&A)
       : "memory");
 }
 
-// Eight outputs of one row: scale, bias, activation, bf16.  Kept out of line: inlined at all 16
+// Four outputs of one row: scale, bias, activation, bf16.  Kept out of line: inlined at all 16
 // call sites of the epilogue the activation code would be tens of KB of instructions.
-struct F8 {
-  float v[8];
+struct F4 {
+  float v[4];
 };
-__device__ __attribute__((noinline)) uint4 epilogue8(F8 y, F8 sc, F8 bi, int act) {
-  uint32_t o[4];
+__device__ __attribute__((noinline)) uint2 epilogue4(F4 y, F4 sc, F4 bi, int act) {
+  uint32_t o[2];
 #pragma unroll
-  for (int c = 0; c < 8; c += 2) {
+  for (int c = 0; c < 4; c += 2) {
     const uint32_t lo = f32_to_bf16(act_fast(y.v[c] * sc.v[c] + bi.v[c], act));
     const uint32_t hi = f32_to_bf16(act_fast(y.v[c + 1] * sc.v[c + 1] + bi.v[c + 1], act));
     o[c / 2] = lo | (hi << 16);
   }
-  return make_uint4(o[0], o[1], o[2], o[3]);
+  return make_uint2(o[0], o[1]);
 }
 
 template <int WDT>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  // Tile order: the 8 XCDs take workgroups round-robin; consecutive tiles (along N within a row
-  // of tiles) go to one XCD so that they share x rows in its L2.
+  // Tile order: consecutive work items go to one XCD (workgroups are dispatched round-robin over
+  // the 8); with whole 2 x 16 tile groups, 32 consecutive items form one group.
   const int total = gridDim.x;
   const int bid = blockIdx.x;
-  const int tile = (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
-  const int tm = tile / a.tiles_n, tn = tile % a.tiles_n;
+  const int item = (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
+  int tm, tn;
+  if (a.grouped) {
+    const int g = item >> 5, q = item & 31, gpr = a.tiles_n >> 4;
+    tm = 2 * (g / gpr) + (q >> 4);
+    tn = 16 * (g % gpr) + (q & 15);
+  } else {
+    tm = item / a.tiles_n;
+    tn = item % a.tiles_n;
+  }
   const int m0 = tm * kBM, n0 = tn * kBN;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wr = wave & 3, wc = wave >> 2;
   const int cg = lane & 15, kq = lane >> 4;
   const int KB = a.K / kBK;
 
-  // DMA sources.  x: this wave issues stage chunks q = 64*(8*wave + i) + lane; chunk q holds row
+  // DMA sources.  x: this wave issues stage chunks q = 64*(4*wave + i) + lane; chunk q holds row
   // r = q / 8, k-chunk (q % 8) ^ ((r >> 1) & 7).  Rows past M read row M-1.
   const uint16_t* asrc[kAInstr];
 #pragma unroll
@@ -136,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     const int r = q >> 3, c = (q & 7) ^ ((r >> 1) & 7);
     asrc[i] = a.x + (size_t)min(m0 + r, a.M - 1) * a.K + 8 * c;
   }
-  // w: this wave issues 8-row blocks t = 2*wave + i; lane L loads row 8t + L/8, 16-byte chunk L%8.
+  // w: this wave issues 8-row block t = wave; lane L loads row 8t + L/8, 16-byte chunk L%8.
   // Chunks past N read column 0 (their outputs are not stored).
   const uint8_t* bsrc[kBInstr];
 #pragma unroll
@@ -153,16 +166,16 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       dma16(bsrc[i] + (size_t)kb * kBK * a.N, st + kABytes + (kBInstr * wave + i) * kBPitch);
   };
 
-  f32x4_t acc[4][8];
+  f32x4_t acc[4][4];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < 4; ++c) acc[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Lane parts of the LDS read addresses (x row 64*wave + i of the first row block, w rows).
+  // Lane parts of the LDS read addresses (x row 64*wr + i of the first row block, w columns).
   const int i16 = lane & 15;
-  const uint32_t a_row = (uint32_t)((64 * wave + i16) * (kBK * 2));
-  const uint32_t b_lane = (uint32_t)(kABytes + 8 * cg);
+  const uint32_t a_row = (uint32_t)((64 * wr + i16) * (kBK * 2));
+  const uint32_t b_lane = (uint32_t)(kABytes + 64 * wc + 4 * cg);
 
   for (int s = 0; s < kStages; ++s)
     if (s < KB) issue(s, smem + s * kStage);
@@ -183,18 +196,18 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       const uint32_t aa = sb + a_row + (uint32_t)((c ^ (i16 >> 1)) * 16);
       const uint32_t ba = sb + b_lane + (uint32_t)((4 * sub + kq) * kBPitch);
       u32x4_v A[4];
-      u32x2_v Bq[8];
+      uint32_t Bq[8];
       read_step(aa, ba, A, Bq);
-      // B operands: column c of this lane's 8, rows 8*kq + 0..7 as four bf16 pairs.
-      u32x4_v B[8];
+      // B operands: column c of this lane's 4, rows 8*kq + 0..7 as four bf16 pairs.
+      u32x4_v B[4];
 #pragma unroll
-      for (int col = 0; col < 8; ++col) {
-        const int dw = col >> 2, sh = 8 * (col & 3);
+      for (int col = 0; col < 4; ++col) {
+        const int sh = 8 * col;
         uint32_t p[4];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-          const uint32_t lo = dw ? Bq[2 * pp].y : Bq[2 * pp].x;
-          const uint32_t hi = dw ? Bq[2 * pp + 1].y : Bq[2 * pp + 1].x;
+          const uint32_t lo = Bq[2 * pp];
+          const uint32_t hi = Bq[2 * pp + 1];
           float f0, f1;
           if constexpr (WDT == MX_DTYPE_INT8) {
             f0 = (float)(int8_t)(lo >> sh);
@@ -210,18 +223,18 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-        for (int col = 0; col < 8; ++col) acc[rb][col] = mfma(A[rb], B[col], acc[rb][col]);
+        for (int col = 0; col < 4; ++col) acc[rb][col] = mfma(A[rb], B[col], acc[rb][col]);
     }
     __builtin_amdgcn_s_barrier();  // every wave has read this stage
     if (kb + kStages < KB) issue(kb + kStages, st);
   }
 
-  // Epilogue: y = act(acc * s[n] + bias[n]) for this lane's 8 columns.
-  const int ncol = n0 + 8 * cg;
+  // Epilogue: y = act(acc * s[n] + bias[n]) for this lane's 4 columns.
+  const int ncol = n0 + 64 * wc + 4 * cg;
   if (ncol >= a.N) return;
-  F8 sc, bi;
+  F4 sc, bi;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
+  for (int c = 0; c < 4; ++c) {
     sc.v[c] = load_f(a.scale, ncol + c, a.s_dt);
     bi.v[c] = a.bias ? load_f(a.bias, ncol + c, a.b_dt) : 0.0f;
   }
@@ -229,12 +242,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = m0 + 64 * wave + 16 * rb + 4 * kq + r;
+      const int row = m0 + 64 * wr + 16 * rb + 4 * kq + r;
       if (row < a.M) {
-        F8 y;
+        F4 y;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) y.v[c] = acc[rb][c][r];
-        *(uint4*)(a.out + (size_t)row * a.N + ncol) = epilogue8(y, sc, bi, a.act);
+        for (int c = 0; c < 4; ++c) y.v[c] = acc[rb][c][r];
+        *(uint2*)(a.out + (size_t)row * a.N + ncol) = epilogue4(y, sc, bi, a.act);
       }
     }
   }
@@ -268,6 +281,7 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   if (tiles_m * tiles_n > (int64_t)1 << 30)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: output too large for the GEMM path");
   ga.tiles_n = (int)tiles_n;
+  ga.grouped = (tiles_m % 2 == 0 && tiles_n % 16 == 0) ? 1 : 0;
   const int grid = (int)(tiles_m * tiles_n);
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
