@@ -105,18 +105,18 @@ int dot_run(mx_backend* b, const DotDesc& d) {
   switch (d.in_dt) {
     case MX_DTYPE_FLOAT32:
       return launch(b, "dot_tiled_f32", [&] {
-        dot_tiled_kernel<float, float><<<grid, 256, 0, st>>>((const float*)d.lhs, (const float*)d.rhs, (float*)d.out, d.M,
+        dispatch(dot_tiled_kernel<float, float>, grid, 256, 0, st, (const float*)d.lhs, (const float*)d.rhs, (float*)d.out, d.M,
                                                               d.K, d.N, d.rhs_transposed, d.in_dt);
       });
     case MX_DTYPE_FLOAT64:
       return launch(b, "dot_tiled_f64", [&] {
-        dot_tiled_kernel<double, double><<<grid, 256, 0, st>>>((const double*)d.lhs, (const double*)d.rhs,
+        dispatch(dot_tiled_kernel<double, double>, grid, 256, 0, st, (const double*)d.lhs, (const double*)d.rhs,
                                                                 (double*)d.out, d.M, d.K, d.N, d.rhs_transposed, d.in_dt);
       });
     case MX_DTYPE_BFLOAT16:
     case MX_DTYPE_FLOAT16:
       return launch(b, d.in_dt == MX_DTYPE_BFLOAT16 ? "dot_tiled_bf16" : "dot_tiled_f16", [&] {
-        dot_tiled_kernel<uint16_t, float><<<grid, 256, 0, st>>>((const uint16_t*)d.lhs, (const uint16_t*)d.rhs,
+        dispatch(dot_tiled_kernel<uint16_t, float>, grid, 256, 0, st, (const uint16_t*)d.lhs, (const uint16_t*)d.rhs,
                                                                  (float*)d.out, d.M, d.K, d.N, d.rhs_transposed, d.in_dt);
       });
     default:

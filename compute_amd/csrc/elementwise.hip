@@ -121,7 +121,7 @@ __global__ void convert_kernel(const void* in, int in_dt, void* out, int out_dt,
 
 int ew_convert(mx_backend* b, const void* in, int in_dt, void* out, int out_dt, int64_t n) {
   if (n == 0) return MX_OK;
-  return launch(b, "convert", [&] { convert_kernel<<<ew_blocks(n), kEwThreads, 0, b->stream>>>(in, in_dt, out, out_dt, n); });
+  return launch(b, "convert", [&] { dispatch(convert_kernel, ew_blocks(n), kEwThreads, 0, b->stream, in, in_dt, out, out_dt, n); });
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -164,7 +164,7 @@ __global__ void unary_kernel(int op, const void* in, void* out, int dt, int64_t 
 
 int ew_unary(mx_backend* b, int optype, const void* in, void* out, int dt, int64_t n) {
   if (n == 0) return MX_OK;
-  return launch(b, "unary", [&] { unary_kernel<<<ew_blocks(n), kEwThreads, 0, b->stream>>>(optype, in, out, dt, n); });
+  return launch(b, "unary", [&] { dispatch(unary_kernel, ew_blocks(n), kEwThreads, 0, b->stream, optype, in, out, dt, n); });
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -246,7 +246,7 @@ int ew_binary(mx_backend* b, int optype, const void* lhs, const int64_t* lhs_dim
     n *= out_dims[a];
   }
   if (n == 0) return MX_OK;
-  return launch(b, "binary", [&] { binary_kernel<<<ew_blocks(n), kEwThreads, 0, b->stream>>>(optype, lhs, rhs, out, d, dt, n); });
+  return launch(b, "binary", [&] { dispatch(binary_kernel, ew_blocks(n), kEwThreads, 0, b->stream, optype, lhs, rhs, out, d, dt, n); });
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -286,10 +286,10 @@ int ew_gather_strided(mx_backend* b, const void* in, void* out, int elem_bytes, 
   if (n == 0) return MX_OK;
   hipStream_t st = b->stream;
   switch (elem_bytes) {
-    case 1: return launch(b, "gather", [&] { gather_kernel<uint8_t><<<ew_blocks(n), kEwThreads, 0, st>>>((const uint8_t*)in, (uint8_t*)out, d, n); });
-    case 2: return launch(b, "gather", [&] { gather_kernel<uint16_t><<<ew_blocks(n), kEwThreads, 0, st>>>((const uint16_t*)in, (uint16_t*)out, d, n); });
-    case 4: return launch(b, "gather", [&] { gather_kernel<uint32_t><<<ew_blocks(n), kEwThreads, 0, st>>>((const uint32_t*)in, (uint32_t*)out, d, n); });
-    case 8: return launch(b, "gather", [&] { gather_kernel<uint64_t><<<ew_blocks(n), kEwThreads, 0, st>>>((const uint64_t*)in, (uint64_t*)out, d, n); });
+    case 1: return launch(b, "gather", [&] { dispatch(gather_kernel<uint8_t>, ew_blocks(n), kEwThreads, 0, st, (const uint8_t*)in, (uint8_t*)out, d, n); });
+    case 2: return launch(b, "gather", [&] { dispatch(gather_kernel<uint16_t>, ew_blocks(n), kEwThreads, 0, st, (const uint16_t*)in, (uint16_t*)out, d, n); });
+    case 4: return launch(b, "gather", [&] { dispatch(gather_kernel<uint32_t>, ew_blocks(n), kEwThreads, 0, st, (const uint32_t*)in, (uint32_t*)out, d, n); });
+    case 8: return launch(b, "gather", [&] { dispatch(gather_kernel<uint64_t>, ew_blocks(n), kEwThreads, 0, st, (const uint64_t*)in, (uint64_t*)out, d, n); });
     default: return set_error(MX_ERR_NOT_IMPLEMENTED, "data movement of packed sub-byte dtypes is not implemented");
   }
 }
@@ -386,10 +386,10 @@ int ew_reduce(mx_backend* b, int optype, const void* in, void* out, int dt, cons
   if (nout > 0x7FFFFFFF) return set_error(MX_ERR_INVALID, "Reduce: too many outputs");
   hipStream_t s = b->stream;
   if (dt == MX_DTYPE_FLOAT64)
-    return launch(b, "reduce", [&] { reduce_kernel<double><<<(unsigned)nout, 256, 0, s>>>(optype, in, out, dt, d); });
+    return launch(b, "reduce", [&] { dispatch(reduce_kernel<double>, (unsigned)nout, 256, 0, s, optype, in, out, dt, d); });
   if (dtype_is_float(dt))
-    return launch(b, "reduce", [&] { reduce_kernel<float><<<(unsigned)nout, 256, 0, s>>>(optype, in, out, dt, d); });
-  return launch(b, "reduce", [&] { reduce_kernel<int64_t><<<(unsigned)nout, 256, 0, s>>>(optype, in, out, dt, d); });
+    return launch(b, "reduce", [&] { dispatch(reduce_kernel<float>, (unsigned)nout, 256, 0, s, optype, in, out, dt, d); });
+  return launch(b, "reduce", [&] { dispatch(reduce_kernel<int64_t>, (unsigned)nout, 256, 0, s, optype, in, out, dt, d); });
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -408,7 +408,7 @@ int ew_iota(mx_backend* b, void* out, int dt, const int64_t* dims, int rank, int
   for (int a = 0; a < rank; ++a) n *= dims[a];
   for (int a = axis + 1; a < rank; ++a) inner *= dims[a];
   if (n == 0) return MX_OK;
-  return launch(b, "iota", [&] { iota_kernel<<<ew_blocks(n), kEwThreads, 0, b->stream>>>(out, dt, inner, dims[axis], n); });
+  return launch(b, "iota", [&] { dispatch(iota_kernel, ew_blocks(n), kEwThreads, 0, b->stream, out, dt, inner, dims[axis], n); });
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -451,7 +451,7 @@ int ew_bias_act(mx_backend* b, const void* in, void* out, int dt, const void* bi
   if (n == 0) return MX_OK;
   if (dt != MX_DTYPE_FLOAT32 && dt != MX_DTYPE_FLOAT64 && dt != MX_DTYPE_BFLOAT16)
     return set_error(MX_ERR_NOT_IMPLEMENTED, "FusedDense: dtype %s", dtype_name(dt));
-  return launch(b, "bias_act", [&] { bias_act_kernel<<<ew_blocks(n), kEwThreads, 0, b->stream>>>(in, out, dt, bias, cols, n, act); });
+  return launch(b, "bias_act", [&] { dispatch(bias_act_kernel, ew_blocks(n), kEwThreads, 0, b->stream, in, out, dt, bias, cols, n, act); });
 }
 
 __global__ void gelu_kernel(const void* in, void* out, int dt, int64_t n, int exact) {
@@ -483,7 +483,7 @@ __global__ void gelu_kernel(const void* in, void* out, int dt, int64_t n, int ex
 
 int ew_gelu(mx_backend* b, const void* in, void* out, int dt, int64_t n, int exact) {
   if (n == 0) return MX_OK;
-  return launch(b, "gelu", [&] { gelu_kernel<<<ew_blocks(n), kEwThreads, 0, b->stream>>>(in, out, dt, n, exact); });
+  return launch(b, "gelu", [&] { dispatch(gelu_kernel, ew_blocks(n), kEwThreads, 0, b->stream, in, out, dt, n, exact); });
 }
 
 }  // namespace mx

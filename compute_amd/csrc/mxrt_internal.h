@@ -2,6 +2,7 @@
 // the MI355X backend. Nothing here crosses the C ABI (see include/mxrt.h for that).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -151,24 +152,42 @@ void dev_free(mx_backend* b, void* p);
 // Ensures scratch has at least `bytes` (zero-filled on growth). Returns the device pointer.
 int ensure_scratch(mx_backend* b, size_t bytes, void** out);
 
-// Launch wrapper: records a hipEvent pair around the launch when profiling is on, and checks
-// the launch status.
+// Launch wrapper: when profiling is on, the kernel launched inside `fn` (through dispatch())
+// carries a start/stop event pair that the runtime stamps with the kernel's own execution
+// interval (hipExtLaunchKernel), so the recorded duration is the kernel's, as a profiler reports
+// it, without the gap of separately recorded events.  Checks the launch status.
 template <typename F>
 int launch(mx_backend* b, const char* name, F&& fn);
 
-int timing_begin(mx_backend* b, hipEvent_t* start);
-int timing_end(mx_backend* b, const char* name, hipEvent_t start);
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+// The events for the launch in progress on this thread (null when not profiling).
+extern thread_local LaunchEvents g_launch_events;
+
+int timing_begin(mx_backend* b, LaunchEvents* ev);
+int timing_end(mx_backend* b, const char* name, const LaunchEvents& ev);
 
 template <typename F>
 int launch(mx_backend* b, const char* name, F&& fn) {
-  hipEvent_t ev = nullptr;
+  LaunchEvents ev;
   if (b->profiling) MX_TRY(timing_begin(b, &ev));
+  g_launch_events = ev;
   fn();
+  g_launch_events = LaunchEvents{};
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(MX_ERR_HIP, "launch of %s failed: %s", name, hipGetErrorString(e));
   if (b->profiling) MX_TRY(timing_end(b, name, ev));
   return MX_OK;
+}
+
+// Kernel launch on `st` (used inside launch()'s callback): kernel<<<grid, block, lds, st>>>(args)
+// with the current profiling events attached.
+template <typename... KArgs, typename... Args>
+void dispatch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t st, Args&&... args) {
+  hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, st, g_launch_events.start, g_launch_events.stop, 0u,
+                        static_cast<KArgs>(args)...);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -169,7 +169,7 @@ int qdense_run(mx_backend* b, const QDenseDesc& d) {
       dim3 grid((unsigned)((d.N + kExactThreads - 1) / kExactThreads),
                 (unsigned)((d.M + kExactRows - 1) / kExactRows));
       if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "FusedQuantizedDense: M too large for the exact path");
-      return launch(b, name, [&] { qdense_exact_kernel<<<grid, kExactThreads, 0, st>>>(d); });
+      return launch(b, name, [&] { dispatch(qdense_exact_kernel, grid, kExactThreads, 0, st, d); });
     }
   }
 }

@@ -286,9 +286,9 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     if (d.w_dt == MX_DTYPE_INT8)
-      qdense_gemm_kernel<MX_DTYPE_INT8><<<grid, kThreads, kLds, st>>>(ga);
+      dispatch(qdense_gemm_kernel<MX_DTYPE_INT8>, grid, kThreads, kLds, st, ga);
     else
-      qdense_gemm_kernel<MX_DTYPE_UINT8><<<grid, kThreads, kLds, st>>>(ga);
+      dispatch(qdense_gemm_kernel<MX_DTYPE_UINT8>, grid, kThreads, kLds, st, ga);
   });
 }
 

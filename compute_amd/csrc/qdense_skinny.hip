@@ -9,34 +9,36 @@
 // The products x*w are exact in f32 (bf16 x, |w| <= 255), so only the summation order differs
 // from the reference loop.
 //
-// The kernel is HBM-bound: every weight byte is read once.  Weights stream from HBM straight
-// into LDS with direct global->LDS loads (16 bytes per lane, no registers involved), so each
-// wave keeps several K steps in flight in a private LDS ring; a step is then read from LDS and
-// dequantised in registers into the B operand of v_mfma_f32_16x16x32_bf16 (the matrix cores do
-// the multiply-adds, the VALU only converts).  The 16 rows of the MFMA A operand are the rows of
-// x (rows >= M repeat row M-1 and are never stored).
+// The kernel is HBM-bound: every weight byte is read once.  It is "one-shot": every wave issues
+// all of its loads at entry (T steps of 32 K rows, T = 1, 2 or 4), straight into registers, so
+// the whole matrix is requested at once and each wave computes a step as soon as that step's
+// data has arrived.  A step is dequantised in registers into the B operand of
+// v_mfma_f32_16x16x32_bf16 (the matrix cores do the multiply-adds, the VALU only converts); the
+// 16 rows of the A operand are the rows of x (rows >= M repeat row M-1 and are never stored).
 //
-// Lane layout (wave of 64 lanes, cg = lane % 16, kq = lane / 16; CPL = columns per lane, 4, 8 or
-// 16, so a workgroup covers 16*CPL columns).  In one 32-row K step a lane uses rows
-// k0 + 8*kq + e (e = 0..7) of its CPL consecutive columns col0 = CPL*cg.  MFMA number c takes
-// column col0 + c from every lane, so its result column j = cg is block column CPL*j + c, and the
-// lane ends up holding rows 4*kq + r (r = 0..3) of its own CPL columns.
+// Lane layout (wave of 64 lanes, cg = lane % 16, kq = lane / 16).  A lane reads 8 bytes of each
+// of the rows k0 + 8*kq + e (e = 0..7) of a 32-row step: 16 int4 or 8 int8 columns (CPL), so a
+// wave covers 16*CPL columns (256 or 128) and each row segment a wave reads is 128 contiguous
+// bytes.  MFMA number c takes column col0 + c from every lane, so its result column j = cg is
+// column CPL*j + c of the block, and the lane ends up holding rows 4*kq + r (r = 0..3) of its
+// own CPL columns.
 //
 // Dequantisation into bf16 pairs (two K rows of one column per dword):
-//   int8/uint8: exact conversion through f32 (|w| < 256 has at most 8 significant bits), the
-//               two high halves packed with one v_perm;
-//   int4/uint4: v_perm gathers the bytes of two rows, then and/xor turn a nibble u into the
-//               bf16 bit pattern 0x4300|u = 128 + u (exact); for Int4 the xor also flips bit 3,
-//               giving 136 + w.  The offset is removed per group with the group's row sums of
-//               x, which one extra MFMA against an all-ones B operand produces.
+//   int8/uint8: exact conversion through f32 (a byte has at most 8 significant bits; the signed
+//               byte is selected and sign-extended by the conversion itself), the two high
+//               halves packed with one v_perm;
+//   int4/uint4: v_perm gathers the bytes of two rows, then and-or turns a nibble u into the
+//               bf16 bit pattern 0x4300|u = 128 + u (exact); Int4 first flips bit 3 of every
+//               nibble, giving 136 + w.  The offset is removed once per group with the group's
+//               row sums of x, which one extra MFMA against an all-ones B operand produces.
 //
-// Work decomposition.  A workgroup (NW = 16, 8 or 4 waves for CPL = 4, 8, 16) owns 16*CPL output
-// columns and one of S slices of the K steps; its waves split the slice's steps.  The host picks
-// CPL and S so that about one workgroup per CU covers the matrix, preferring S = 1 (no split-K)
-// and then narrow column blocks over more slices.  The waves' partial tiles are summed through LDS; with S > 1 every
-// workgroup stores its tile to scratch and the last one to arrive for the column block adds the
-// S tiles in slice order (deterministic), adds the bias, applies the activation and rounds to
-// bf16.
+// Work decomposition.  The K steps of a column block are dealt out T at a time to waves, in
+// order; a workgroup of NW = 8 waves takes NW consecutive wave-chunks (one K slice), so a
+// column block has S = ceil(K/32 / (T*NW)) slices.  T divides the steps of a scale group, so a
+// wave stays inside one group and applies the group scale once, at its end.  The waves'
+// partial tiles are summed through LDS in wave order; with S > 1 every workgroup stores its
+// tile to scratch and the last one to arrive for the column block adds the S tiles in slice
+// order (deterministic), adds the bias, applies the activation and rounds to bf16.
 #include <algorithm>
 #include <cmath>
 
@@ -49,11 +51,11 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-typedef __attribute__((address_space(1))) void* gbl_void_ptr;
 
 constexpr int kSkMaxRows = 16;
-constexpr int kSkRingBytes = 144 * 1024;  // LDS rings of a workgroup (one workgroup per CU)
+constexpr int kSkWaves = 8;
+constexpr int kSkThreads = 64 * kSkWaves;
+constexpr int kSkLaneBytes = 8;  // bytes of one weight row per lane
 
 struct SkinnyArgs {
   const uint16_t* x;    // [M, K] bf16
@@ -62,40 +64,21 @@ struct SkinnyArgs {
   const void* bias;     // [N] or null
   uint16_t* out;        // [M, N] bf16
   float* partial;       // [S, M, N] (S > 1)
-  uint32_t* counters;   // [column blocks]
-  int M, K, N, G, S, act, b_dt;
+  uint32_t* counters;   // [column blocks], zero between launches
+  int M, K, N, G, S, act, s_dt, b_dt;
 };
 
-// Geometry of one instantiation: CPL columns per lane, NW waves per workgroup.  Narrow blocks
-// take more waves, so that each CU has enough waves to overlap one wave's step latency (DMA
-// wait, LDS reads, conversion, MFMA, group flush) with the others' work.
-template <int WDT, int CPL, int NW>
-struct SkGeom {
-  static constexpr bool kI4 = WDT == MX_DTYPE_INT4 || WDT == MX_DTYPE_UINT4;
-  static constexpr int kCols = 16 * CPL;                     // columns per workgroup
-  static constexpr int kRowBytes = kI4 ? kCols / 2 : kCols;  // bytes of one K row of the block
-  static constexpr int kLaneBytes = kRowBytes / 16;          // bytes per lane per row (4/8/16)
-  static constexpr int kWBytes = 32 * kRowBytes;             // weight bytes per 32-row step
-  static constexpr int kWInstr = kWBytes / 1024;             // 16-byte-per-lane DMA loads
-  static constexpr int kSlot = kWBytes + 2048;               // + x block (1 KB) + scales (1 KB)
-  static constexpr int kD0 = kSkRingBytes / (NW * kSlot);
-  static constexpr int kD = kD0 > 7 ? 7 : kD0;               // steps in flight per wave
-  static constexpr int kP = kWInstr + 2;                     // DMA instructions per step
-  static constexpr int kRing = NW * kD * kSlot;              // LDS of the workgroup's rings
-  static constexpr int kThreads = 64 * NW;
-  static_assert(kLaneBytes == 4 || kLaneBytes == 8 || kLaneBytes == 16, "lane width");
-  static_assert(kD >= 2 && kD <= 7 && (kD - 1) * kP < 64, "ring depth");
-};
-
-__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
-  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+__device__ __forceinline__ f32x4_t sk_mfma(const u32x4_v& a, const u32x4_v& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
 }
 
-__device__ __forceinline__ f32x4_t mfma16x16x32(const uint32_t (&a)[4], const uint32_t (&b)[4], f32x4_t c) {
-  const u32x4_v av = {a[0], a[1], a[2], a[3]};
-  const u32x4_v bv = {b[0], b[1], b[2], b[3]};
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), __builtin_bit_cast(bf16x8_t, bv),
-                                                 c, 0, 0, 0);
+// A uniform constant held in a VGPR: (t & mask) | c then selects one v_and_or_b32 (a VOP3
+// instruction takes no literal and at most one scalar operand here).
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t x) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(x));
+  return r;
 }
 
 // Workgroup index -> work item, so that the S slices of one column block (consecutive items)
@@ -105,390 +88,235 @@ __device__ __forceinline__ int sk_xcd_swizzle(int bid, int total) {
   return (bid & 7) * (total >> 3) + (bid >> 3);
 }
 
-// Split-K completion for the partial tiles in scratch.  Every access to the shared partials is
-// an agent-scope atomic (coherent across the XCDs' L2s without whole-cache maintenance); the
-// s_waitcnt makes this workgroup's partial stores complete before its arrival is counted, and
-// only the last arriver reads them back.  Returns true in every thread of the last arriver.
-__device__ __forceinline__ bool sk_last_arriver(uint32_t* counter, uint32_t arrivals, int* s_flag) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == arrivals - 1u;
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = last;
-  }
-  __syncthreads();
-  return *s_flag != 0;
-}
-
-// One wave-wide direct load of 16 bytes per lane from global memory into LDS: lane L's bytes land
-// at lds + 16*L (the LDS address must be the same in every lane).  The data does not pass
-// through registers; completion is tracked by the wave's vmcnt like any vector load.
-__device__ __forceinline__ void dma16(const void* src, void* lds) {
-  __builtin_amdgcn_global_load_lds((gbl_void_ptr)const_cast<void*>(src), (lds_void_ptr)lds, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt not waited for).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Byte address of an LDS location (the value a ds_read takes).
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// LDS reads of one step's operands: 8 rows of this lane's weight bytes (row pitch 16*W) and its
-// 16 bytes of x, issued back to back and completed together.  They are one asm block because
-// the compiler, seeing ordinary LDS reads after LDS-DMA loads, would wait for every outstanding
-// DMA (vmcnt(0)) before them and serialise the ring; the DMA into the slot is known complete
-// from the caller's explicit vmcnt wait.
-template <int W>
-__device__ __forceinline__ void lds_read_step(uint32_t wa, uint32_t xa, uint32_t (&r)[8][W / 4], u32x4_v& x);
-
-template <>
-__device__ __forceinline__ void lds_read_step<4>(uint32_t wa, uint32_t xa, uint32_t (&r)[8][1], u32x4_v& x) {
-  asm volatile(
-      "ds_read_b32 %0, %9 offset:0\n\t"
-      "ds_read_b32 %1, %9 offset:64\n\t"
-      "ds_read_b32 %2, %9 offset:128\n\t"
-      "ds_read_b32 %3, %9 offset:192\n\t"
-      "ds_read_b32 %4, %9 offset:256\n\t"
-      "ds_read_b32 %5, %9 offset:320\n\t"
-      "ds_read_b32 %6, %9 offset:384\n\t"
-      "ds_read_b32 %7, %9 offset:448\n\t"
-      "ds_read_b128 %8, %10 offset:0\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[0][0]), "=&v"(r[1][0]), "=&v"(r[2][0]), "=&v"(r[3][0]), "=&v"(r[4][0]), "=&v"(r[5][0]),
-        "=&v"(r[6][0]), "=&v"(r[7][0]), "=&v"(x)
-      : "v"(wa), "v"(xa)
-      : "memory");
-}
-
-template <>
-__device__ __forceinline__ void lds_read_step<8>(uint32_t wa, uint32_t xa, uint32_t (&r)[8][2], u32x4_v& x) {
-  u32x2_v q[8];
-  asm volatile(
-      "ds_read_b64 %0, %9 offset:0\n\t"
-      "ds_read_b64 %1, %9 offset:128\n\t"
-      "ds_read_b64 %2, %9 offset:256\n\t"
-      "ds_read_b64 %3, %9 offset:384\n\t"
-      "ds_read_b64 %4, %9 offset:512\n\t"
-      "ds_read_b64 %5, %9 offset:640\n\t"
-      "ds_read_b64 %6, %9 offset:768\n\t"
-      "ds_read_b64 %7, %9 offset:896\n\t"
-      "ds_read_b128 %8, %10 offset:0\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]), "=&v"(q[7]),
-        "=&v"(x)
-      : "v"(wa), "v"(xa)
-      : "memory");
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    r[e][0] = q[e].x;
-    r[e][1] = q[e].y;
-  }
-}
-
-template <>
-__device__ __forceinline__ void lds_read_step<16>(uint32_t wa, uint32_t xa, uint32_t (&r)[8][4], u32x4_v& x) {
-  u32x4_v q[8];
-  asm volatile(
-      "ds_read_b128 %0, %9 offset:0\n\t"
-      "ds_read_b128 %1, %9 offset:256\n\t"
-      "ds_read_b128 %2, %9 offset:512\n\t"
-      "ds_read_b128 %3, %9 offset:768\n\t"
-      "ds_read_b128 %4, %9 offset:1024\n\t"
-      "ds_read_b128 %5, %9 offset:1280\n\t"
-      "ds_read_b128 %6, %9 offset:1536\n\t"
-      "ds_read_b128 %7, %9 offset:1792\n\t"
-      "ds_read_b128 %8, %10 offset:0\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]), "=&v"(q[7]),
-        "=&v"(x)
-      : "v"(wa), "v"(xa)
-      : "memory");
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    r[e][0] = q[e].x;
-    r[e][1] = q[e].y;
-    r[e][2] = q[e].z;
-    r[e][3] = q[e].w;
-  }
-}
-
-// The scale bytes of this lane's columns (NB = 8, 16, 32 or 64 bytes) from LDS.
-template <int NB>
-__device__ __forceinline__ void lds_read_scales(uint32_t sa, uint32_t (&s)[NB / 4]) {
-  if constexpr (NB == 8) {
-    u32x2_v v;
-    asm volatile("ds_read_b64 %0, %1 offset:0\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(sa) : "memory");
-    s[0] = v.x;
-    s[1] = v.y;
-  } else {
-    u32x4_v q[NB / 16];
-    if constexpr (NB == 16) {
-      asm volatile("ds_read_b128 %0, %1 offset:0\n\ts_waitcnt lgkmcnt(0)" : "=&v"(q[0]) : "v"(sa) : "memory");
-    } else if constexpr (NB == 32) {
-      asm volatile("ds_read_b128 %0, %2 offset:0\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
-                   : "=&v"(q[0]), "=&v"(q[1])
-                   : "v"(sa)
-                   : "memory");
-    } else {
-      asm volatile(
-          "ds_read_b128 %0, %4 offset:0\n\tds_read_b128 %1, %4 offset:16\n\t"
-          "ds_read_b128 %2, %4 offset:32\n\tds_read_b128 %3, %4 offset:48\n\ts_waitcnt lgkmcnt(0)"
-          : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
-          : "v"(sa)
-          : "memory");
-    }
-#pragma unroll
-    for (int i = 0; i < NB / 16; ++i) {
-      s[4 * i] = q[i].x;
-      s[4 * i + 1] = q[i].y;
-      s[4 * i + 2] = q[i].z;
-      s[4 * i + 3] = q[i].w;
-    }
-  }
-}
-
-// Waves per workgroup for a lane width.
-template <int CPL>
-constexpr int sk_waves() {
-  return CPL == 4 ? 16 : (CPL == 8 ? 8 : 4);
-}
-
-template <int WDT, int SDT, int CPL, int NW>
-__global__ __launch_bounds__(64 * NW) void qdense_skinny_kernel(SkinnyArgs a) {
-  using Gm = SkGeom<WDT, CPL, NW>;
-  constexpr bool kI4 = Gm::kI4;
+// WDT: weight dtype.  T: K steps per wave (divides the steps of a scale group).  MR: rows of the
+// MFMA result kept per lane (1 when M == 1, else 4).
+template <int WDT, int T, int MR>
+__global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a) {
+  constexpr bool kI4 = WDT == MX_DTYPE_INT4 || WDT == MX_DTYPE_UINT4;
+  constexpr int CPL = kI4 ? 2 * kSkLaneBytes : kSkLaneBytes;  // columns per lane
+  constexpr int kCols = 16 * CPL;                              // columns per workgroup
+  constexpr int kSLoads = CPL * 4 / 16;  // 16-byte scale loads per lane (f32 size; bf16 repeats)
   constexpr float kOff = WDT == MX_DTYPE_INT4 ? 136.0f : (WDT == MX_DTYPE_UINT4 ? 128.0f : 0.0f);
-  constexpr uint32_t kNibXor = WDT == MX_DTYPE_INT4 ? 0x43084308u : 0x43004300u;
-  constexpr int kSB = SDT == MX_DTYPE_BFLOAT16 ? 2 : 4;  // scale bytes
-  constexpr int kD = Gm::kD;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  extern __shared__ __attribute__((aligned(16))) float red[];
   __shared__ int s_last;
 
   const int item = sk_xcd_swizzle(blockIdx.x, gridDim.x);
   const int cb = item / a.S, slice = item % a.S;
-  // The wave index is wave-uniform; saying so keeps the K loop's control flow scalar.
+  // The wave index is wave-uniform; saying so keeps the control flow scalar.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int cg = lane & 15, kq = lane >> 4;
-  const int T = a.K >> 5;
-  const int sb = (int)((int64_t)slice * T / a.S), se = (int)((int64_t)(slice + 1) * T / a.S);
-  const int wb = sb + wave * (se - sb) / NW, we = sb + (wave + 1) * (se - sb) / NW;
-  uint8_t* ring = smem + (size_t)wave * kD * Gm::kSlot;
-  const int cblk = cb * Gm::kCols;
+  const int KS = a.K >> 5;
+  const int wb = (slice * kSkWaves + wave) * T;  // first K step of this wave
+  const int cblk = cb * kCols;
+  const int col0 = cblk + cg * CPL;
 
-  // DMA source addresses of this lane.  Chunks past the last column read column 0 instead
-  // (their results are never stored), so no load needs a predicate.
-  const size_t row_bytes = kI4 ? (size_t)(a.N >> 1) : (size_t)a.N;
-  const size_t blk_bytes = kI4 ? (size_t)(cblk >> 1) : (size_t)cblk;
-  const uint8_t* wsrc[Gm::kWInstr];
+  float tot[CPL][MR];
 #pragma unroll
-  for (int i = 0; i < Gm::kWInstr; ++i) {
-    const int f = i * 1024 + lane * 16;  // byte of the step's row-major [32][kRowBytes] tile
-    const int r = f / Gm::kRowBytes, ch = f % Gm::kRowBytes;
-    const size_t cbyte = blk_bytes + ch + 16 <= row_bytes ? blk_bytes + ch : 0;
-    wsrc[i] = a.w + (size_t)r * row_bytes + cbyte;
-  }
-  const uint16_t* xsrc = a.x + (size_t)min(lane & 15, a.M - 1) * a.K + 8 * (lane >> 4);
-  const size_t s_row = (size_t)a.N * kSB;
-  const size_t s_byte = (size_t)cblk * kSB + lane * 16;
-  const char* ssrc = (const char*)a.scale + (s_byte + 16 <= s_row ? s_byte : 0);
-
-  auto issue = [&](int j, uint8_t* slot) {
-    const size_t step = (size_t)(32 * j) * row_bytes;
+  for (int c = 0; c < CPL; ++c)
 #pragma unroll
-    for (int i = 0; i < Gm::kWInstr; ++i) dma16(wsrc[i] + step, slot + i * 1024);
-    dma16(xsrc + 32 * j, slot + Gm::kWBytes);
-    dma16(ssrc + (size_t)((32 * j) / a.G) * s_row, slot + Gm::kWBytes + 1024);
-  };
+    for (int r = 0; r < MR; ++r) tot[c][r] = 0.0f;
 
-  f32x4_t tot[CPL], grp[CPL], sx;
+  // The host makes K/32 a multiple of T, so a wave has T steps or none; with a fixed count the
+  // loads are one straight-line sequence and every step waits only for its own data.
+  if (wb < KS) {
+    // Lanes whose columns lie past N read column 0 instead (their results are never stored).
+    const size_t row_bytes = kI4 ? (size_t)(a.N >> 1) : (size_t)a.N;
+    const size_t lbyte = (kI4 ? (size_t)(col0 >> 1) : (size_t)col0);
+    const uint8_t* wp = a.w + (size_t)(32 * wb + 8 * kq) * row_bytes + (lbyte + kSkLaneBytes <= row_bytes ? lbyte : 0);
+    const uint16_t* xp = a.x + (size_t)min(cg, a.M - 1) * a.K + 32 * wb + 8 * kq;
+    const int sb = a.s_dt == MX_DTYPE_BFLOAT16 ? 2 : 4;
+    const int scol = col0 < a.N ? col0 : 0;
+    const char* sp = (const char*)a.scale + ((size_t)((32 * wb) / a.G) * a.N + scol) * sb;
+    const int s_last_load = CPL * sb / 16 - 1;
+
+    u32x4_v xv[T];
+    u32x2_v wv[T][8];
+    u32x4_v sv[kSLoads];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    tot[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    grp[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-  sx = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  // Lane offsets of the LDS reads inside a slot.
-  const uint32_t w_off = (uint32_t)(8 * kq * Gm::kRowBytes + cg * Gm::kLaneBytes);
-  const uint32_t x_off = (uint32_t)(Gm::kWBytes + lane * 16);
-  const uint32_t s_off = (uint32_t)(Gm::kWBytes + 1024 + cg * CPL * kSB);
-
-  auto compute_step = [&](int j, const uint8_t* slot) {
-    // The group's sums are folded into the totals after its last step (or after the wave's last
-    // step when the wave's range ends inside a group).
-    const bool flush = (j + 1 == we) || ((32 * (j + 1)) % a.G == 0);
-    const uint32_t sbase = lds_addr(slot);
-    uint32_t r[8][Gm::kLaneBytes / 4], xv[4];
-    {
-      u32x4_v xq;
-      lds_read_step<Gm::kLaneBytes>(sbase + w_off, sbase + x_off, r, xq);
-      xv[0] = xq.x;
-      xv[1] = xq.y;
-      xv[2] = xq.z;
-      xv[3] = xq.w;
+    for (int t = 0; t < T; ++t) {
+      xv[t] = *(const u32x4_v*)(xp + 32 * t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        wv[t][e] = __builtin_nontemporal_load((const u32x2_v*)(wp + (size_t)(32 * t + e) * row_bytes));
     }
-    if constexpr (kI4) {
+    // The group's scales last: they are needed only after the last step.  Always kSLoads loads
+    // (bf16 scales repeat their last one), so the number of loads in flight is fixed.
 #pragma unroll
-      for (int d = 0; d < CPL / 8; ++d) {
-        uint32_t bq[8][4];  // columns 8d + 0..7, four pair-dwords each
+    for (int q = 0; q < kSLoads; ++q) sv[q] = *(const u32x4_v*)(sp + 16 * min(q, s_last_load));
+    // Keep every load above this point: the scheduler would otherwise interleave later steps'
+    // loads with earlier steps' arithmetic to save registers, and serialise their latencies.
+    __builtin_amdgcn_sched_barrier(0);
+
+    const uint32_t kMask = 0x000F000Fu;
+    const uint32_t kOr = vgpr_const(0x43004300u);
+    const u32x4_v ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+    const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4_t grp[CPL], sx = zero;
 #pragma unroll
-        for (int pp = 0; pp < 4; ++pp) {
-          const uint32_t A = r[2 * pp][d], B = r[2 * pp + 1][d];
-          const uint32_t t0 = __builtin_amdgcn_perm(B, A, 0x06040200u);  // [A.b0, A.b2, B.b0, B.b2]
-          const uint32_t t1 = __builtin_amdgcn_perm(B, A, 0x07050301u);  // [A.b1, A.b3, B.b1, B.b3]
-          bq[0][pp] = ((t0 >> 0) & 0x000F000Fu) ^ kNibXor;
-          bq[1][pp] = ((t0 >> 4) & 0x000F000Fu) ^ kNibXor;
-          bq[4][pp] = ((t0 >> 8) & 0x000F000Fu) ^ kNibXor;
-          bq[5][pp] = ((t0 >> 12) & 0x000F000Fu) ^ kNibXor;
-          bq[2][pp] = ((t1 >> 0) & 0x000F000Fu) ^ kNibXor;
-          bq[3][pp] = ((t1 >> 4) & 0x000F000Fu) ^ kNibXor;
-          bq[6][pp] = ((t1 >> 8) & 0x000F000Fu) ^ kNibXor;
-          bq[7][pp] = ((t1 >> 12) & 0x000F000Fu) ^ kNibXor;
+    for (int t = 0; t < T; ++t) {
+      if constexpr (kI4) {
+#pragma unroll
+        for (int d = 0; d < CPL / 8; ++d) {
+          uint32_t bq[8][4];  // columns 8d + 0..7, four pair-dwords each
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) {
+            uint32_t A = wv[t][2 * pp][d], B = wv[t][2 * pp + 1][d];
+            if constexpr (WDT == MX_DTYPE_INT4) {
+              A ^= 0x88888888u;
+              B ^= 0x88888888u;
+            }
+            const uint32_t t0 = __builtin_amdgcn_perm(B, A, 0x06040200u);  // [A.b0, A.b2, B.b0, B.b2]
+            const uint32_t t1 = __builtin_amdgcn_perm(B, A, 0x07050301u);  // [A.b1, A.b3, B.b1, B.b3]
+            bq[0][pp] = (t0 & kMask) | kOr;
+            bq[1][pp] = ((t0 >> 4) & kMask) | kOr;
+            bq[4][pp] = ((t0 >> 8) & kMask) | kOr;
+            bq[5][pp] = ((t0 >> 12) & kMask) | kOr;
+            bq[2][pp] = (t1 & kMask) | kOr;
+            bq[3][pp] = ((t1 >> 4) & kMask) | kOr;
+            bq[6][pp] = ((t1 >> 8) & kMask) | kOr;
+            bq[7][pp] = ((t1 >> 12) & kMask) | kOr;
+          }
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+            grp[8 * d + c] = sk_mfma(xv[t], u32x4_v{bq[c][0], bq[c][1], bq[c][2], bq[c][3]}, t == 0 ? zero : grp[8 * d + c]);
         }
+        sx = sk_mfma(xv[t], ones, t == 0 ? zero : sx);
+      } else {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) grp[8 * d + c] = mfma16x16x32(xv, bq[c], grp[8 * d + c]);
+        for (int d = 0; d < CPL / 4; ++d) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            uint32_t bq[4];
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+              const uint32_t r0 = wv[t][2 * pp][d], r1 = wv[t][2 * pp + 1][d];
+              float f0, f1;
+              if constexpr (WDT == MX_DTYPE_INT8) {
+                f0 = (float)(int8_t)(r0 >> (8 * c));
+                f1 = (float)(int8_t)(r1 >> (8 * c));
+              } else {
+                f0 = (float)(uint8_t)(r0 >> (8 * c));
+                f1 = (float)(uint8_t)(r1 >> (8 * c));
+              }
+              bq[pp] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+            }
+            grp[4 * d + c] = sk_mfma(xv[t], u32x4_v{bq[0], bq[1], bq[2], bq[3]}, t == 0 ? zero : grp[4 * d + c]);
+          }
+        }
       }
-      const uint32_t ones[4] = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-      sx = mfma16x16x32(xv, ones, sx);
+    }
+    // The group's scale, once: tot = (grp - offset * rowsum(x)) * s.
+    float sc[CPL];
+    if (a.s_dt == MX_DTYPE_BFLOAT16) {
+#pragma unroll
+      for (int c = 0; c < CPL; c += 2) {
+        const uint32_t v = sv[c / 8][(c / 2) % 4];
+        sc[c] = __uint_as_float(v << 16);
+        sc[c + 1] = __uint_as_float(v & 0xFFFF0000u);
+      }
     } else {
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        const int dw = c >> 2, sh = 8 * (c & 3);
-        uint32_t bq[4];
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp) {
-          float f0, f1;
-          if constexpr (WDT == MX_DTYPE_INT8) {
-            f0 = (float)(int8_t)(r[2 * pp][dw] >> sh);
-            f1 = (float)(int8_t)(r[2 * pp + 1][dw] >> sh);
-          } else {
-            f0 = (float)(uint8_t)(r[2 * pp][dw] >> sh);
-            f1 = (float)(uint8_t)(r[2 * pp + 1][dw] >> sh);
-          }
-          bq[pp] = pack_hi16(f0, f1);
-        }
-        grp[c] = mfma16x16x32(xv, bq, grp[c]);
-      }
+      for (int c = 0; c < CPL; ++c) sc[c] = __uint_as_float(sv[c / 4][c % 4]);
     }
-    if (flush) {
-      uint32_t sv[CPL * kSB / 4];
-      lds_read_scales<CPL * kSB>(sbase + s_off, sv);
-      float sc[CPL];
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        if constexpr (SDT == MX_DTYPE_BFLOAT16)
-          sc[c] = __uint_as_float((c & 1) ? (sv[c >> 1] & 0xFFFF0000u) : (sv[c >> 1] << 16));
-        else
-          sc[c] = __uint_as_float(sv[c]);
-      }
+    for (int c = 0; c < CPL; ++c)
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float v = kOff != 0.0f ? grp[c][q] - kOff * sx[q] : grp[c][q];
-          tot[c][q] += v * sc[c];
-        }
-        grp[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      }
-      sx = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-
-  // Pipeline: kD steps in flight per wave.  Step j's DMA has completed once at most
-  // (number of steps issued after it) * kP vector-memory instructions are outstanding; its
-  // slot is refilled with step j + kD after it has been read.
-  for (int d = 0; d < kD; ++d)
-    if (wb + d < we) issue(wb + d, ring + d * Gm::kSlot);
-  for (int j = wb; j < we; ++j) {
-    uint8_t* slot = ring + ((j - wb) % kD) * Gm::kSlot;
-    const int newer = min(kD - 1, we - 1 - j);
-    switch (newer) {  // ring tail: fewer steps were issued after this one
-      case 0: wait_vmcnt<0>(); break;
-      case 1: wait_vmcnt<Gm::kP>(); break;
-      case 2: wait_vmcnt<(kD > 2 ? 2 : 0) * Gm::kP>(); break;
-      case 3: wait_vmcnt<(kD > 3 ? 3 : 0) * Gm::kP>(); break;
-      case 4: wait_vmcnt<(kD > 4 ? 4 : 0) * Gm::kP>(); break;
-      case 5: wait_vmcnt<(kD > 5 ? 5 : 0) * Gm::kP>(); break;
-      default: wait_vmcnt<(kD > 6 ? 6 : 0) * Gm::kP>(); break;
-    }
-    compute_step(j, slot);  // its LDS reads have completed (lgkmcnt(0) inside)
-    if (j + kD < we) issue(j + kD, slot);
+      for (int r = 0; r < MR; ++r) tot[c][r] = (kOff != 0.0f ? grp[c][r] - kOff * sx[r] : grp[c][r]) * sc[c];
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();  // the rings are reused below
 
-  // Every wave's tile (rows < M) into LDS as [NW waves][M][cols] (the rings' memory); then the
-  // block's M x cols outputs are shared out over the threads, each adding the waves in a fixed
-  // order.  A thread's outputs all lie in one column (the thread count is a multiple of the
-  // block width), so its bias is loaded once.
-  constexpr int kC = Gm::kCols;
-  float* red = (float*)smem;
+  // Every wave's tile (rows < M) into LDS as [waves][M][kCols]; each output then adds the waves
+  // in a fixed order.  Thread t owns outputs p = t + i * kSkThreads of the block's M x kCols.
   const int M = a.M;
   {
-    float* rw = red + (size_t)wave * M * kC;
+    float* rw = red + (size_t)wave * M * kCols;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = 4 * kq + q;
+    for (int r = 0; r < MR; ++r) {
+      const int row = 4 * kq + r;
       if (row < M) {
 #pragma unroll
         for (int c = 0; c < CPL; c += 4)
-          *(float4*)(rw + row * kC + cg * CPL + c) = make_float4(tot[c][q], tot[c + 1][q], tot[c + 2][q], tot[c + 3][q]);
+          *(float4*)(rw + row * kCols + cg * CPL + c) = make_float4(tot[c][r], tot[c + 1][r], tot[c + 2][r], tot[c + 3][r]);
       }
     }
   }
   __syncthreads();
-  constexpr int kThreads = Gm::kThreads;
-  static_assert(kThreads % kC == 0, "one column per thread");
+  constexpr int kMaxOut = kSkMaxRows * kCols / kSkThreads;
   const int t = threadIdx.x;
-  const int MC = M * kC;
-  const int n_t = cblk + t % kC;
-  const float bias_t = (a.bias && n_t < a.N) ? load_f(a.bias, n_t, a.b_dt) : 0.0f;
-  auto finish = [&](int p, float y) {
-    const int m = p / kC;
-    if (n_t < a.N) a.out[(size_t)m * a.N + n_t] = f32_to_bf16(act_fast(y + bias_t, a.act));
-  };
-  auto wave_sum = [&](int p) {
-    float v = red[p];
+  const int MC = M * kCols;
+  float own[kMaxOut];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) v += red[w * MC + p];
-    return v;
+  for (int i = 0; i < kMaxOut; ++i) {
+    const int p = t + i * kSkThreads;
+    float v = 0.0f;
+    if (p < MC) {
+      v = red[p];
+#pragma unroll
+      for (int w = 1; w < kSkWaves; ++w) v += red[w * MC + p];
+    }
+    own[i] = v;
+  }
+  auto finish = [&](int i, float y) {
+    const int p = t + i * kSkThreads;
+    const int m = p / kCols, n = cblk + p % kCols;
+    if (n < a.N) {
+      const float b = a.bias ? load_f(a.bias, n, a.b_dt) : 0.0f;
+      a.out[(size_t)m * a.N + n] = f32_to_bf16(act_fast(y + b, a.act));
+    }
   };
   if (a.S == 1) {
-    for (int p = t; p < MC; p += kThreads) finish(p, wave_sum(p));
+#pragma unroll
+    for (int i = 0; i < kMaxOut; ++i)
+      if (t + i * kSkThreads < MC) finish(i, own[i]);
     return;
   }
-  for (int p = t; p < MC; p += kThreads) {
-    const int m = p / kC, n = cblk + p % kC;
-    if (n < a.N)
-      __hip_atomic_store(&a.partial[((size_t)slice * M + m) * a.N + n], wave_sum(p), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-  }
-  if (!sk_last_arriver(&a.counters[cb], (uint32_t)a.S, &s_last)) return;
-  // Last arriver: each output adds the S slices in slice order, 8 loads in flight at a time.
-  for (int p = t; p < MC; p += kThreads) {
-    const int m = p / kC;
-    const int n = min(n_t, a.N - 1);
-    const float* src = a.partial + (size_t)m * a.N + n;
-    const size_t ss = (size_t)M * a.N;
-    float y = 0.0f;
-    for (int s0 = 0; s0 < a.S; s0 += 8) {
-      float pv[8];
+
+  // Split K: store this slice's tile (agent-scope relaxed atomics: coherent across the XCDs'
+  // L2s without whole-cache maintenance), wait until the stores have completed, then count the
+  // arrival.  Only the last arriver reads the tiles back.
+  const size_t ss = (size_t)M * a.N;
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        pv[u] = __hip_atomic_load(src + (size_t)min(s0 + u, a.S - 1) * ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) y += s0 + u < a.S ? pv[u] : 0.0f;
-    }
-    finish(p, y);
+  for (int i = 0; i < kMaxOut; ++i) {
+    const int p = t + i * kSkThreads;
+    const int m = p / kCols, n = cblk + p % kCols;
+    if (p < MC && n < a.N)
+      __hip_atomic_store(&a.partial[slice * ss + (size_t)m * a.N + n], own[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&a.counters[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == (uint32_t)a.S - 1u;
+    if (last) __hip_atomic_store(&a.counters[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // Last arriver: y = sum over slices in slice order.  The loads of kChunk slices of all of this
+  // thread's outputs are issued together (one memory round trip per chunk).
+  constexpr int kChunk = kMaxOut >= 8 ? 4 : 8;
+  float y[kMaxOut];
+#pragma unroll
+  for (int i = 0; i < kMaxOut; ++i) y[i] = 0.0f;
+  for (int s0 = 0; s0 < a.S; s0 += kChunk) {
+    float v[kChunk][kMaxOut];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u)
+#pragma unroll
+      for (int i = 0; i < kMaxOut; ++i) {
+        const int s = min(s0 + u, a.S - 1);
+        const int p = min(t + i * kSkThreads, MC - 1);
+        const int m = p / kCols, n = min(cblk + p % kCols, a.N - 1);
+        v[u][i] = __hip_atomic_load(&a.partial[s * ss + (size_t)m * a.N + n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u)
+#pragma unroll
+      for (int i = 0; i < kMaxOut; ++i)
+        if (s0 + u < a.S) y[i] += s0 + u == slice ? own[i] : v[u][i];
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxOut; ++i)
+    if (t + i * kSkThreads < MC) finish(i, y[i]);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -503,72 +331,42 @@ bool qdense_skinny_fits(const QDenseDesc& d) {
          aligned(d.w, 16) && aligned(d.x, 16) && aligned(d.scale, 16);
 }
 
-// Columns per lane and number of K slices.  Each option covers the columns with 16*CPL-wide
-// blocks and takes S = floor(CUs / blocks) slices (at least 1), so about one workgroup per CU
-// (the rings take most of a CU's LDS).  The best option fills the most CUs in its last round;
-// ties go to fewer slices (no split-K is best: no partials, no completion protocol), then to
-// wider blocks.
-struct SkPlan {
-  int cpl = 16, S = 1;
-};
-
-static SkPlan skinny_plan(const QDenseDesc& d, int num_cus) {
-  const bool i4 = dtype_is_packed(d.w_dt);
-  const int64_t cus = std::max(num_cus, 1);
-  const int64_t steps = d.K / 32;
-  SkPlan best;
-  double best_u = -1.0;
-  for (int cpl : {16, 8, 4}) {
-    if (i4 && cpl == 4) continue;
-    const int64_t nb = (d.N + 16 * cpl - 1) / (16 * cpl);
-    int64_t S = std::max<int64_t>(1, cus / nb);
-    const int nw = cpl == 4 ? 16 : (cpl == 8 ? 8 : 4);
-    S = std::min<int64_t>(S, std::max<int64_t>(1, steps / (2 * nw)));  // each wave keeps >= 2 steps
-    S = std::min<int64_t>(S, std::max<int64_t>(1, 120 / d.M));
-    const int64_t wgs = nb * S;
-    const int64_t rounds = (wgs + cus - 1) / cus;
-    const double u = (double)wgs / (double)(rounds * cus);
-    if (u > best_u + 1e-9 || (std::fabs(u - best_u) <= 1e-9 && S < best.S)) {
-      best_u = u;
-      best.cpl = cpl;
-      best.S = (int)S;
-    }
-  }
-  return best;
+// Steps per wave: the largest of 4, 2, 1 that divides both the K steps and the steps of a scale
+// group (a per-output-channel scale is one group spanning K).
+static int skinny_steps_per_wave(const QDenseDesc& d) {
+  const int64_t ks = d.K / 32;
+  const int64_t G = std::min<int64_t>(d.block_size, d.K);
+  const int64_t spg = G >= d.K ? ks : G / 32;
+  for (int t : {4, 2})
+    if (ks % t == 0 && spg % t == 0) return t;
+  return 1;
 }
 
-template <int WDT, int SDT, int CPL>
-static void launch_one(const SkinnyArgs& ga, int grid, hipStream_t st) {
-  constexpr int NW = sk_waves<CPL>();
-  using Gm = SkGeom<WDT, CPL, NW>;
-  // The rings; after the K loop the same memory holds the waves' tiles (NW x M rows).
-  const size_t lds = std::max<size_t>(Gm::kRing, (size_t)NW * ga.M * Gm::kCols * sizeof(float));
-  qdense_skinny_kernel<WDT, SDT, CPL, NW><<<grid, Gm::kThreads, lds, st>>>(ga);
-}
-
-template <int WDT, int SDT>
-static void launch_cpl(const SkinnyArgs& ga, int cpl, int grid, hipStream_t st) {
-  if (cpl == 16) {
-    launch_one<WDT, SDT, 16>(ga, grid, st);
-  } else if (cpl == 8) {
-    launch_one<WDT, SDT, 8>(ga, grid, st);
-  } else {
-    if constexpr (WDT == MX_DTYPE_INT8 || WDT == MX_DTYPE_UINT8) launch_one<WDT, SDT, 4>(ga, grid, st);
-  }
+template <int WDT, int T>
+static void launch_t(const SkinnyArgs& ga, int grid, size_t lds, hipStream_t st) {
+  if (ga.M == 1)
+    dispatch(qdense_skinny_kernel<WDT, T, 1>, grid, kSkThreads, lds, st, ga);
+  else
+    dispatch(qdense_skinny_kernel<WDT, T, 4>, grid, kSkThreads, lds, st, ga);
 }
 
 template <int WDT>
-static void launch_skinny(const SkinnyArgs& ga, int cpl, int grid, int sdt, hipStream_t st) {
-  if (sdt == MX_DTYPE_BFLOAT16)
-    launch_cpl<WDT, MX_DTYPE_BFLOAT16>(ga, cpl, grid, st);
+static void launch_skinny(const SkinnyArgs& ga, int T, int grid, size_t lds, hipStream_t st) {
+  if (T == 4)
+    launch_t<WDT, 4>(ga, grid, lds, st);
+  else if (T == 2)
+    launch_t<WDT, 2>(ga, grid, lds, st);
   else
-    launch_cpl<WDT, MX_DTYPE_FLOAT32>(ga, cpl, grid, st);
+    launch_t<WDT, 1>(ga, grid, lds, st);
 }
 
 int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
-  const SkPlan plan = skinny_plan(d, b->num_cus);
-  const int64_t nb = (d.N + 16 * plan.cpl - 1) / (16 * plan.cpl);
-  const int S = plan.S;
+  const bool i4 = dtype_is_packed(d.w_dt);
+  const int64_t cols = i4 ? 256 : 128;
+  const int64_t nb = (d.N + cols - 1) / cols;
+  const int T = skinny_steps_per_wave(d);
+  const int64_t chunks = d.K / 32 / T;  // wave-sized pieces of one column block
+  const int64_t S = (chunks + kSkWaves - 1) / kSkWaves;
   const size_t counter_bytes = 64 * 1024;
   if ((size_t)nb * 4 > counter_bytes || nb * S > (int64_t)1 << 30)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: N=%lld too large for the skinny path", (long long)d.N);
@@ -590,17 +388,19 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.K = (int)d.K;
   ga.N = (int)d.N;
   ga.G = (int)std::min<int64_t>(d.block_size, d.K);
-  ga.S = S;
+  ga.S = (int)S;
   ga.act = d.act;
+  ga.s_dt = d.s_dt;
   ga.b_dt = d.b_dt;
   const int grid = (int)(nb * S);
+  const size_t lds = (size_t)kSkWaves * d.M * cols * sizeof(float);
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     switch (d.w_dt) {
-      case MX_DTYPE_INT4: launch_skinny<MX_DTYPE_INT4>(ga, plan.cpl, grid, d.s_dt, st); break;
-      case MX_DTYPE_UINT4: launch_skinny<MX_DTYPE_UINT4>(ga, plan.cpl, grid, d.s_dt, st); break;
-      case MX_DTYPE_INT8: launch_skinny<MX_DTYPE_INT8>(ga, plan.cpl, grid, d.s_dt, st); break;
-      default: launch_skinny<MX_DTYPE_UINT8>(ga, plan.cpl, grid, d.s_dt, st); break;
+      case MX_DTYPE_INT4: launch_skinny<MX_DTYPE_INT4>(ga, T, grid, lds, st); break;
+      case MX_DTYPE_UINT4: launch_skinny<MX_DTYPE_UINT4>(ga, T, grid, lds, st); break;
+      case MX_DTYPE_INT8: launch_skinny<MX_DTYPE_INT8>(ga, T, grid, lds, st); break;
+      default: launch_skinny<MX_DTYPE_UINT8>(ga, T, grid, lds, st); break;
     }
   });
 }

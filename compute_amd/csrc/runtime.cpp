@@ -239,17 +239,16 @@ static int get_event(mx_backend* b, hipEvent_t* ev) {
   return MX_OK;
 }
 
-int timing_begin(mx_backend* b, hipEvent_t* start) {
-  MX_TRY(get_event(b, start));
-  MX_CHECK_HIP(hipEventRecord(*start, b->stream));
+thread_local LaunchEvents g_launch_events;
+
+int timing_begin(mx_backend* b, LaunchEvents* ev) {
+  MX_TRY(get_event(b, &ev->start));
+  MX_TRY(get_event(b, &ev->stop));
   return MX_OK;
 }
 
-int timing_end(mx_backend* b, const char* name, hipEvent_t start) {
-  hipEvent_t stop;
-  MX_TRY(get_event(b, &stop));
-  MX_CHECK_HIP(hipEventRecord(stop, b->stream));
-  b->pending.push_back(PendingTiming{name, start, stop});
+int timing_end(mx_backend* b, const char* name, const LaunchEvents& ev) {
+  b->pending.push_back(PendingTiming{name, ev.start, ev.stop});
   return MX_OK;
 }
 
