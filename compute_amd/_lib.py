@@ -126,6 +126,7 @@ SIGNATURES = {
     "mx_exec_execute": [_P, C.POINTER(_P), C.POINTER(C.c_uint8), _I, C.POINTER(_P), _I],
     "mx_exec_finalize": [_P],
     "mx_exec_execute_loop": [_P, C.POINTER(_P), _I, _I, _I],
+    "mx_exec_describe": [_P, C.c_char_p, _SZ],
     "mx_qdense": [_P, C.POINTER(mx_qdense_args)],
     "mx_qdense_plan": [_P, C.POINTER(mx_qdense_args), C.c_char_p, _SZ],
 }

@@ -608,6 +608,12 @@ class Executable:
             out.append(_from_c_shape(s))
         return out
 
+    def Describe(self) -> list:
+        """The operations Execute runs, in order, after compile-time fusion (mx_exec_describe)."""
+        buf = C.create_string_buffer(1 << 16)
+        _check(self._lib.mx_exec_describe(self._h, buf, len(buf)))
+        return [l for l in buf.value.decode().split("\n") if l]
+
     def Execute(self, inputs: Sequence[Buffer], donate: Optional[Sequence[bool]] = None, defaultDevice: int = 0):
         n = len(inputs)
         arr = (C.c_void_p * max(1, n))(*[b._h.value if b is not None else None for b in inputs])

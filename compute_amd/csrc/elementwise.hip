@@ -487,3 +487,69 @@ int ew_gelu(mx_backend* b, const void* in, void* out, int dt, int64_t n, int exa
 }
 
 }  // namespace mx
+
+namespace mx {
+
+// ---------------------------------------------------------------------------------------------
+// Row RMS normalisation (the graph compiler's fusion of the op chain written out in
+// mxrt_internal.h).  One workgroup per row.  The sum of squares is accumulated exactly as the
+// separate ReduceSum kernel accumulates it (256 threads, strided partial sums, then a tree in
+// LDS), and every product and sum is rounded on its own (no contraction), so the result equals
+// the unfused graph's bit for bit.
+// ---------------------------------------------------------------------------------------------
+// Rows of up to kRmsCached * 256 elements are read once into registers (all loads issued
+// before the first use); longer rows are read twice.
+constexpr int kRmsCached = 32;
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const float* c, const float* e, uint16_t* out,
+                                                     int64_t D) {
+  __shared__ float sh[256];
+  const int64_t m = blockIdx.x;
+  const uint16_t* xr = x + m * D;
+  const int t = threadIdx.x;
+  const bool cached = D <= (int64_t)kRmsCached * 256;
+  float v[kRmsCached];
+  float acc = 0.0f;
+  if (cached) {
+    // Unconditional loads (clamped index) so that they are all in flight together; the values
+    // past the row end are not used.
+#pragma unroll
+    for (int i = 0; i < kRmsCached; ++i) v[i] = bf16_to_f32(xr[min(t + 256 * (int64_t)i, D - 1)]);
+#pragma unroll
+    for (int i = 0; i < kRmsCached; ++i)
+      if (t + 256 * (int64_t)i < D) acc = add_rn(acc, mul_rn(v[i], v[i]));
+  } else {
+    for (int64_t d = t; d < D; d += 256) {
+      const float w = bf16_to_f32(xr[d]);
+      acc = add_rn(acc, mul_rn(w, w));
+    }
+  }
+  sh[t] = acc;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (t < s) sh[t] = add_rn(sh[t], sh[t + s]);
+    __syncthreads();
+  }
+  const float tt = add_rn(mul_rn(sh[0], c[m]), e[m]);
+  const float inv = (float)(1.0 / sqrt((double)tt));
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kRmsCached; ++i) {
+      const int64_t d = t + 256 * (int64_t)i;
+      if (d < D) out[m * D + d] = f32_to_bf16(mul_rn(v[i], inv));
+    }
+  } else {
+    for (int64_t d = t; d < D; d += 256) out[m * D + d] = f32_to_bf16(mul_rn(bf16_to_f32(xr[d]), inv));
+  }
+}
+
+int ew_rmsnorm(mx_backend* b, const void* x, const void* c, const void* e, void* out, int64_t M, int64_t D) {
+  if (M == 0 || D == 0) return MX_OK;
+  if (M > 0x7FFFFFFF) return set_error(MX_ERR_INVALID, "RMS normalisation: too many rows");
+  return launch(b, "rmsnorm", [&] {
+    dispatch(rmsnorm_kernel, (unsigned)M, 256, 0, b->stream, (const uint16_t*)x, (const float*)c, (const float*)e,
+             (uint16_t*)out, D);
+  });
+}
+
+}  // namespace mx

@@ -40,6 +40,7 @@ enum class Op {
   kBiasAct,
   kGelu,
   kCopy,
+  kRmsNorm,  // fused row RMS normalisation (compile-time fusion)
 };
 
 static const char* op_name(Op op) {
@@ -59,6 +60,7 @@ static const char* op_name(Op op) {
     case Op::kBiasAct: return "BiasActivation";
     case Op::kGelu: return "FusedGelu";
     case Op::kCopy: return "Copy";
+    case Op::kRmsNorm: return "RmsNorm";
   }
   return "?";
 }
@@ -76,6 +78,7 @@ struct Node {
   // FusedQuantizedDense.
   int scheme = 0, block_axis = 0, block_size = 0, act = 0;
   bool has_zp = false, has_bias = false;
+  int res_op = 0;  // elementwise op folded into the epilogue (operand = last input)
   int64_t M = 0, K = 0, N = 0;
   // DotNorm.
   int64_t B = 0;
@@ -961,6 +964,123 @@ int mx_fn_slice(mx_function* fn, mx_value xv, const int64_t* starts, const int64
 // ---------------------------------------------------------------------------------------------
 // Compile.
 // ---------------------------------------------------------------------------------------------
+// ---------------------------------------------------------------------------------------------
+// Compile-time fusion.  Rewrites patterns into fewer kernels with identical arithmetic (every
+// intermediate is rounded exactly as the separate ops round it); nodes left without consumers
+// are dropped by the liveness analysis that follows.
+// ---------------------------------------------------------------------------------------------
+static std::vector<int> count_uses(const FunctionImpl& f, const std::vector<Node>& nodes) {
+  std::vector<int> uses(nodes.size(), 0);
+  for (const Node& n : nodes)
+    for (int j : n.in) ++uses[j];
+  for (int o : f.outputs) ++uses[o];
+  return uses;
+}
+
+static bool is_binary_op(const Node& n, int optype) { return n.op == Op::kBinary && n.optype == optype; }
+// A binary node without broadcasting (both operands have the output's dims).
+static bool same_shape_binary(const Node& n) { return n.in_dims == n.shape.dims && n.in2_dims == n.shape.dims; }
+
+// FusedQuantizedDense followed by Add or Mul with a same-shape tensor: the op moves into the
+// dense kernel's epilogue (the binary node becomes the dense node, the original dense node loses
+// its only consumer).
+static void fuse_dense_epilogues(const FunctionImpl& f, std::vector<Node>& nodes) {
+  std::vector<int> uses = count_uses(f, nodes);
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    Node& n = nodes[i];
+    if (n.op != Op::kBinary || (n.optype != MX_OP_ADD && n.optype != MX_OP_MUL) || !same_shape_binary(n)) continue;
+    // Prefer the later dense operand, so that the other one is computed before this node.
+    int q = -1, r = -1;
+    for (int side = 1; side >= 0; --side) {
+      const int c = n.in[side];
+      const Node& cn = nodes[c];
+      if (cn.op == Op::kQDense && cn.res_op == 0 && uses[c] == 1 && cn.shape == n.shape) {
+        q = c;
+        r = n.in[1 - side];
+        break;
+      }
+    }
+    if (q < 0) continue;
+    Node fused = nodes[q];
+    fused.in.push_back(r);
+    fused.res_op = n.optype;
+    n = fused;
+    uses = count_uses(f, nodes);
+  }
+}
+
+// RMS normalisation written out with standard ops (as a GoMLX model builds it):
+//   xf = ConvertDType(x bf16 [M, D] -> f32); ss = ReduceSum(Mul(xf, xf), axis 1);
+//   t = Add(Mul(ss, c), e) with c, e f32 [M]; inv = Rsqrt(t);
+//   h = ConvertDType(Mul(xf, BroadcastInDim(inv, [M, D], axes {0})) -> bf16)
+// becomes one RmsNorm(x, c, e) node (commuted operands of the Mul/Add nodes are matched too).
+static void fuse_rms_norm(const FunctionImpl& f, std::vector<Node>& nodes) {
+  std::vector<int> uses = count_uses(f, nodes);
+  auto single = [&](int i) { return uses[i] == 1; };
+  auto f32 = [&](int i) { return nodes[i].shape.dtype == MX_DTYPE_FLOAT32; };
+  for (size_t hi = 0; hi < nodes.size(); ++hi) {
+    const Node& h = nodes[hi];
+    if (h.op != Op::kConvert || h.shape.dtype != MX_DTYPE_BFLOAT16 || h.shape.rank() != 2) continue;
+    const int64_t M = h.shape.dims[0], D = h.shape.dims[1];
+    const int hf = h.in[0];
+    if (!is_binary_op(nodes[hf], MX_OP_MUL) || !f32(hf) || !single(hf) || !same_shape_binary(nodes[hf])) continue;
+    // Mul(xf, invb) in either order.
+    int xf = -1, invb = -1;
+    for (int side = 0; side < 2; ++side) {
+      const int a0 = nodes[hf].in[side], a1 = nodes[hf].in[1 - side];
+      const Node& xn = nodes[a0];
+      const Node& bn = nodes[a1];
+      if (xn.op == Op::kConvert && nodes[xn.in[0]].shape.dtype == MX_DTYPE_BFLOAT16 && bn.op == Op::kGather &&
+          single(a1) && bn.offset == 0 && bn.strides.size() == 2 && (bn.strides[0] == 1 || M == 1) &&
+          bn.strides[1] == 0 &&
+          nodes[bn.in[0]].shape.dims == std::vector<int64_t>{M}) {
+        xf = a0;
+        invb = a1;
+        break;
+      }
+    }
+    if (xf < 0) continue;
+    const int inv = nodes[invb].in[0];
+    if (nodes[inv].op != Op::kUnary || nodes[inv].optype != MX_OP_RSQRT || !f32(inv) || !single(inv)) continue;
+    const int t = nodes[inv].in[0];
+    if (!is_binary_op(nodes[t], MX_OP_ADD) || !single(t) || !same_shape_binary(nodes[t])) continue;
+    // Add(ms, e) and Mul(ss, c), either order; ms must be the Mul, ss the ReduceSum.
+    int ms = -1, e = -1;
+    for (int side = 0; side < 2; ++side)
+      if (is_binary_op(nodes[nodes[t].in[side]], MX_OP_MUL) && single(nodes[t].in[side])) {
+        ms = nodes[t].in[side];
+        e = nodes[t].in[1 - side];
+        break;
+      }
+    if (ms < 0 || !same_shape_binary(nodes[ms])) continue;
+    int ss = -1, c = -1;
+    for (int side = 0; side < 2; ++side) {
+      const int cand = nodes[ms].in[side];
+      const Node& rn = nodes[cand];
+      if (rn.op == Op::kReduce && rn.optype == MX_OP_REDUCE_SUM && single(cand) && rn.mask == 2u &&
+          rn.in_dims == std::vector<int64_t>{M, D}) {
+        ss = cand;
+        c = nodes[ms].in[1 - side];
+        break;
+      }
+    }
+    if (ss < 0) continue;
+    const int sq = nodes[ss].in[0];
+    if (!is_binary_op(nodes[sq], MX_OP_MUL) || !single(sq) || nodes[sq].in[0] != xf || nodes[sq].in[1] != xf) continue;
+    if (!f32(c) || !f32(e) || nodes[c].shape.dims != std::vector<int64_t>{M} ||
+        nodes[e].shape.dims != std::vector<int64_t>{M})
+      continue;
+    Node fused;
+    fused.op = Op::kRmsNorm;
+    fused.shape = h.shape;
+    fused.in = {nodes[xf].in[0], c, e};
+    fused.M = M;
+    fused.N = D;
+    nodes[hi] = fused;
+    uses = count_uses(f, nodes);
+  }
+}
+
 int mx_builder_compile(mx_builder* bld, mx_executable** out) {
   clear_error();
   if (!bld || !out) return set_error(MX_ERR_INVALID, "NULL argument");
@@ -975,6 +1095,10 @@ int mx_builder_compile(mx_builder* bld, mx_executable** out) {
   e->nodes = std::move(bld->fn.nodes);
   e->params = bld->fn.params;
   e->outputs = bld->fn.outputs;
+  if (!b->no_fusion) {
+    fuse_rms_norm(bld->fn, e->nodes);
+    fuse_dense_epilogues(bld->fn, e->nodes);
+  }
   const int nn = (int)e->nodes.size();
 
   // Storage roots: alias ops share their input's storage.
@@ -1129,6 +1253,11 @@ static int run_node(mx_executable* e, int i, std::vector<void*>& ptr) {
       d.block_axis = n.block_axis;
       d.block_size = n.block_size;
       d.act = n.act;
+      if (n.res_op) {
+        d.res = in((int)n.in.size() - 1);
+        d.res_dt = ins((int)n.in.size() - 1).dtype;
+        d.res_op = n.res_op;
+      }
       return qdense_run(b, d);
     }
     case Op::kDotNorm: {
@@ -1163,6 +1292,8 @@ static int run_node(mx_executable* e, int i, std::vector<void*>& ptr) {
       return ew_bias_act(b, in(0), out, n.shape.dtype, n.in.size() > 1 ? in(1) : nullptr, n.M, n.N, n.act);
     case Op::kGelu:
       return ew_gelu(b, in(0), out, n.shape.dtype, count, n.flag & 1);
+    case Op::kRmsNorm:
+      return ew_rmsnorm(b, in(0), in(1), in(2), out, n.M, n.N);
     case Op::kCopy:
       if (n.shape.nbytes())
         MX_CHECK_HIP(hipMemcpyAsync(out, in(0), n.shape.nbytes(), hipMemcpyDeviceToDevice, b->stream));
@@ -1173,6 +1304,23 @@ static int run_node(mx_executable* e, int i, std::vector<void*>& ptr) {
 }
 
 }  // namespace mx
+
+extern "C" int mx_exec_describe(const mx_executable* e, char* buf, size_t buflen) {
+  clear_error();
+  if (!e || !buf || buflen == 0) return set_error(MX_ERR_INVALID, "Describe: NULL argument");
+  std::string s;
+  for (const Node& n : e->nodes) {
+    if (n.flag & 0x100) continue;  // dead
+    if (n.op == Op::kParameter || n.op == Op::kConstant || n.op == Op::kReshape || n.op == Op::kBitcast) continue;
+    s += op_name(n.op);
+    if (n.op == Op::kQDense && n.res_op) s += n.res_op == MX_OP_MUL ? "+Mul" : "+Add";
+    s += "\n";
+  }
+  const size_t k = std::min(buflen - 1, s.size());
+  memcpy(buf, s.data(), k);
+  buf[k] = 0;
+  return MX_OK;
+}
 
 extern "C" int mx_exec_execute(mx_executable* e, mx_buffer* const* inputs, const uint8_t* donate, int n_inputs,
                                mx_buffer** outputs, int n_outputs) {

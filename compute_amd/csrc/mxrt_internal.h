@@ -111,6 +111,7 @@ struct PendingTiming {
 struct mx_backend {
   int device = 0;
   bool host_only = false;
+  bool no_fusion = false;  // "nofusion" option: compile graphs op by op
   bool finalized = false;
   hipStream_t stream = nullptr;
   std::recursive_mutex mu;
@@ -205,6 +206,11 @@ struct QDenseDesc {
   int64_t M, K, N;
   int x_dt, w_dt, s_dt, zp_dt, b_dt;
   int scheme, block_axis, block_size, act;
+  // Optional elementwise epilogue folded in by the graph compiler: out = t OP res, with t the
+  // dense result rounded to its dtype and res a same-shape tensor (op 0 = none; MX_OP_ADD or
+  // MX_OP_MUL), rounded again as the separate elementwise op would.
+  const void* res = nullptr;
+  int res_dt = 0, res_op = 0;
 };
 int qdense_validate(const mx_qdense_args* a, QDenseDesc* d);
 int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name);
@@ -248,5 +254,9 @@ int ew_iota(mx_backend* b, void* out, int dt, const int64_t* dims, int rank, int
 int ew_bias_act(mx_backend* b, const void* in, void* out, int dt, const void* bias, int64_t rows,
                 int64_t cols, int act);
 int ew_gelu(mx_backend* b, const void* in, void* out, int dt, int64_t n, int exact);
+// Row RMS normalisation of bf16 x [M, D] with per-row f32 multiplier c and offset e:
+// out = bf16(f32(x) * rsqrt(sum_d f32(x)^2 * c + e)), each step rounded as the separate ops
+// (ConvertDType, Mul, ReduceSum, Mul, Add, Rsqrt, BroadcastInDim, Mul, ConvertDType) round it.
+int ew_rmsnorm(mx_backend* b, const void* x, const void* c, const void* e, void* out, int64_t M, int64_t D);
 
 }  // namespace mx

@@ -156,6 +156,22 @@ int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name) {
 int qdense_run(mx_backend* b, const QDenseDesc& d) {
   MX_TRY(check_device(b));
   const QPath p = choose_path(d);
+  if (d.res_op != 0 && p != QPath::kSkinny && p != QPath::kEmpty) {
+    // Only the skinny kernel applies a folded elementwise op in its epilogue: elsewhere the dense
+    // result goes to a temporary and the op runs as its own kernel (the same arithmetic).
+    const int64_t dims[2] = {d.M, d.N};
+    const size_t bytes = (size_t)d.M * d.N * (d.x_dt == MX_DTYPE_BFLOAT16 ? 2 : 4);
+    void* tmp = nullptr;
+    MX_TRY(dev_alloc(b, bytes, &tmp));
+    QDenseDesc d2 = d;
+    d2.out = tmp;
+    d2.res = nullptr;
+    d2.res_op = 0;
+    int rc = qdense_run(b, d2);
+    if (rc == MX_OK) rc = ew_binary(b, d.res_op, tmp, dims, d.res, dims, d.out, dims, 2, d.x_dt);
+    dev_free(b, tmp);  // stream-ordered pool: later users run after these kernels
+    return rc;
+  }
   const char* name = path_name(d, p);
   hipStream_t st = b->stream;
   switch (p) {

@@ -65,7 +65,8 @@ struct SkinnyArgs {
   uint16_t* out;        // [M, N] bf16
   float* partial;       // [S, M, N] (S > 1)
   uint32_t* counters;   // [column blocks], zero between launches
-  int M, K, N, G, S, act, s_dt, b_dt;
+  const void* res;      // [M, N] epilogue operand (res_op != 0)
+  int M, K, N, G, S, act, s_dt, b_dt, res_dt, res_op;
 };
 
 __device__ __forceinline__ f32x4_t sk_mfma(const u32x4_v& a, const u32x4_v& b, f32x4_t c) {
@@ -260,7 +261,12 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
     const int m = p / kCols, n = cblk + p % kCols;
     if (n < a.N) {
       const float b = a.bias ? load_f(a.bias, n, a.b_dt) : 0.0f;
-      a.out[(size_t)m * a.N + n] = f32_to_bf16(act_fast(y + b, a.act));
+      uint16_t o = f32_to_bf16(act_fast(y + b, a.act));
+      if (a.res_op) {  // the folded elementwise op, rounded as the separate op rounds it
+        const float r = load_f(a.res, (size_t)m * a.N + n, a.res_dt), v = bf16_to_f32(o);
+        o = f32_to_bf16(a.res_op == MX_OP_MUL ? mul_rn(v, r) : add_rn(v, r));
+      }
+      a.out[(size_t)m * a.N + n] = o;
     }
   };
   if (a.S == 1) {
@@ -392,6 +398,9 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.act = d.act;
   ga.s_dt = d.s_dt;
   ga.b_dt = d.b_dt;
+  ga.res = d.res;
+  ga.res_dt = d.res_dt;
+  ga.res_op = d.res_op;
   const int grid = (int)(nb * S);
   const size_t lds = (size_t)kSkWaves * d.M * cols * sizeof(float);
   hipStream_t st = b->stream;

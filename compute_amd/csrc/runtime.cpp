@@ -292,7 +292,7 @@ int mx_backend_new(const char* config, mx_backend** out) {
   *out = nullptr;
   std::string cfg = config ? config : "";
   int device = 0;
-  bool host_only = false;
+  bool host_only = false, no_fusion = false;
   // Comma-separated options, mirroring the "name:cfg" convention of GOMLX_BACKEND (compute.go:141-147).
   size_t pos = 0;
   while (pos <= cfg.size()) {
@@ -300,6 +300,8 @@ int mx_backend_new(const char* config, mx_backend** out) {
     std::string opt = cfg.substr(pos, comma == std::string::npos ? std::string::npos : comma - pos);
     if (opt == "host_only") {
       host_only = true;
+    } else if (opt == "nofusion") {
+      no_fusion = true;
     } else if (opt.rfind("device=", 0) == 0) {
       char* end = nullptr;
       long v = strtol(opt.c_str() + 7, &end, 10);
@@ -314,6 +316,7 @@ int mx_backend_new(const char* config, mx_backend** out) {
   auto* b = new mx_backend();
   b->device = device;
   b->host_only = host_only;
+  b->no_fusion = no_fusion;
   if (host_only) {
     b->description = "MI355X backend (host_only: graph building only)";
     *out = b;

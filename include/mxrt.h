@@ -308,6 +308,11 @@ int mx_exec_finalize(mx_executable* e);
  * iteration.  Asynchronous like Execute. */
 int mx_exec_execute_loop(mx_executable* e, mx_buffer* const* input_sets, int n_sets, int n_inputs,
                          int iters);
+/* The operations Execute runs, in order, one per line (after compile-time fusion, e.g.
+ * "RmsNorm", "FusedQuantizedDense+Mul"); parameters, constants and storage aliases are not
+ * listed.  Writes at most buflen bytes including the terminating NUL.  No counterpart in the
+ * reference: an inspection aid for callers and tests, like an HLO dump. */
+int mx_exec_describe(const mx_executable* e, char* buf, size_t buflen);
 
 /* ---------------------------------------------------------------------------------------------
  * Direct kernel entry point for the hot path (device pointers; no graph).  The compiled
