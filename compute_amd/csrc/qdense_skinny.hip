@@ -89,10 +89,36 @@ __device__ __forceinline__ int sk_xcd_swizzle(int bid, int total) {
   return (bid & 7) * (total >> 3) + (bid >> 3);
 }
 
-// WDT: weight dtype.  T: K steps per wave (divides the steps of a scale group).  MR: rows of the
-// MFMA result kept per lane (1 when M == 1, else 4).
-template <int WDT, int T, int MR>
-__global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a) {
+// Element idx of a bf16 or f32 array p (null: 0), read as the aligned 32-bit word holding it,
+// so that the load is one unconditional instruction whatever the type (the word never leaves the
+// page of the element).  sk_word issues the load, sk_value picks the element once it has arrived.
+struct SkWord {
+  uint32_t w;
+  uint32_t shift;  // moves a bf16 element into the high half: 16 for the low half, else 0
+};
+
+__device__ __forceinline__ SkWord sk_word(const void* p, size_t idx, int dt, const void* dummy) {
+  const bool bf = dt == MX_DTYPE_BFLOAT16;
+  const char* e = p ? (const char*)p + idx * (bf ? 2 : 4) : (const char*)dummy;
+  const uint32_t mis = (uint32_t)(uintptr_t)e & 3u;
+  return SkWord{*(const uint32_t*)(e - mis), bf ? 16u - 8u * (mis & 2u) : 0u};
+}
+
+__device__ __forceinline__ float sk_value(SkWord v, const void* p, int dt) {
+  if (!p) return 0.0f;
+  return dt == MX_DTYPE_BFLOAT16 ? __uint_as_float((v.w << v.shift) & 0xFFFF0000u) : __uint_as_float(v.w);
+}
+
+// WDT: weight dtype.  T: K steps per wave.  FL: steps per scale group seen by a wave (FL divides
+// T and the steps of a group, so a wave's groups are whole and aligned).  MR: rows of the MFMA
+// result kept per lane (1 when M == 1, else 4).
+// int8 grids have twice as many column blocks as int4 ones: their kernels are held to two
+// workgroups per CU (128 registers) so that a whole grid is resident at once.
+template <int WDT, int T, int FL, int MR>
+__global__ __launch_bounds__(kSkThreads)
+__attribute__((amdgpu_waves_per_eu((WDT == MX_DTYPE_INT8 || WDT == MX_DTYPE_UINT8) ? 4 : 1))) void
+qdense_skinny_kernel(SkinnyArgs a) {
+  static_assert(T % FL == 0, "whole scale groups per wave");
   constexpr bool kI4 = WDT == MX_DTYPE_INT4 || WDT == MX_DTYPE_UINT4;
   constexpr int CPL = kI4 ? 2 * kSkLaneBytes : kSkLaneBytes;  // columns per lane
   constexpr int kCols = 16 * CPL;                              // columns per workgroup
@@ -127,23 +153,29 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
     const uint16_t* xp = a.x + (size_t)min(cg, a.M - 1) * a.K + 32 * wb + 8 * kq;
     const int sb = a.s_dt == MX_DTYPE_BFLOAT16 ? 2 : 4;
     const int scol = col0 < a.N ? col0 : 0;
-    const char* sp = (const char*)a.scale + ((size_t)((32 * wb) / a.G) * a.N + scol) * sb;
+    const char* sp = (const char*)a.scale + (size_t)scol * sb;
     const int s_last_load = CPL * sb / 16 - 1;
 
+    // Per scale group: its steps' x and weights, then its scales (needed only after its last
+    // step), so that a group's flush waits for nothing of the later groups.  Always kSLoads
+    // scale loads (bf16 scales repeat their last one): the number of loads in flight is fixed.
     u32x4_v xv[T];
     u32x2_v wv[T][8];
-    u32x4_v sv[kSLoads];
+    u32x4_v sv[T / FL][kSLoads];
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      xv[t] = *(const u32x4_v*)(xp + 32 * t);
+    for (int f = 0; f < T / FL; ++f) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        wv[t][e] = __builtin_nontemporal_load((const u32x2_v*)(wp + (size_t)(32 * t + e) * row_bytes));
+      for (int tt = 0; tt < FL; ++tt) {
+        const int t = f * FL + tt;
+        xv[t] = *(const u32x4_v*)(xp + 32 * t);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          wv[t][e] = __builtin_nontemporal_load((const u32x2_v*)(wp + (size_t)(32 * t + e) * row_bytes));
+      }
+      const char* sg = sp + (size_t)((32 * (wb + f * FL)) / a.G) * a.N * sb;
+#pragma unroll
+      for (int q = 0; q < kSLoads; ++q) sv[f][q] = *(const u32x4_v*)(sg + 16 * min(q, s_last_load));
     }
-    // The group's scales last: they are needed only after the last step.  Always kSLoads loads
-    // (bf16 scales repeat their last one), so the number of loads in flight is fixed.
-#pragma unroll
-    for (int q = 0; q < kSLoads; ++q) sv[q] = *(const u32x4_v*)(sp + 16 * min(q, s_last_load));
     // Keep every load above this point: the scheduler would otherwise interleave later steps'
     // loads with earlier steps' arithmetic to save registers, and serialise their latencies.
     __builtin_amdgcn_sched_barrier(0);
@@ -154,7 +186,10 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
     const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4_t grp[CPL], sx = zero;
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
+    for (int f = 0; f < T / FL; ++f) {
+#pragma unroll
+    for (int tt = 0; tt < FL; ++tt) {
+      const int t = f * FL + tt;
       if constexpr (kI4) {
 #pragma unroll
         for (int d = 0; d < CPL / 8; ++d) {
@@ -179,9 +214,9 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
           }
 #pragma unroll
           for (int c = 0; c < 8; ++c)
-            grp[8 * d + c] = sk_mfma(xv[t], u32x4_v{bq[c][0], bq[c][1], bq[c][2], bq[c][3]}, t == 0 ? zero : grp[8 * d + c]);
+            grp[8 * d + c] = sk_mfma(xv[t], u32x4_v{bq[c][0], bq[c][1], bq[c][2], bq[c][3]}, tt == 0 ? zero : grp[8 * d + c]);
         }
-        sx = sk_mfma(xv[t], ones, t == 0 ? zero : sx);
+        sx = sk_mfma(xv[t], ones, tt == 0 ? zero : sx);
       } else {
 #pragma unroll
         for (int d = 0; d < CPL / 4; ++d) {
@@ -201,32 +236,35 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
               }
               bq[pp] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
             }
-            grp[4 * d + c] = sk_mfma(xv[t], u32x4_v{bq[0], bq[1], bq[2], bq[3]}, t == 0 ? zero : grp[4 * d + c]);
+            grp[4 * d + c] = sk_mfma(xv[t], u32x4_v{bq[0], bq[1], bq[2], bq[3]}, tt == 0 ? zero : grp[4 * d + c]);
           }
         }
       }
-    }
-    // The group's scale, once: tot = (grp - offset * rowsum(x)) * s.
+      }
+    // The group's scale, once per group: tot += (grp - offset * rowsum(x)) * s.
     float sc[CPL];
     if (a.s_dt == MX_DTYPE_BFLOAT16) {
 #pragma unroll
       for (int c = 0; c < CPL; c += 2) {
-        const uint32_t v = sv[c / 8][(c / 2) % 4];
+        const uint32_t v = sv[f][c / 8][(c / 2) % 4];
         sc[c] = __uint_as_float(v << 16);
         sc[c + 1] = __uint_as_float(v & 0xFFFF0000u);
       }
     } else {
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) sc[c] = __uint_as_float(sv[c / 4][c % 4]);
+      for (int c = 0; c < CPL; ++c) sc[c] = __uint_as_float(sv[f][c / 4][c % 4]);
     }
 #pragma unroll
     for (int c = 0; c < CPL; ++c)
 #pragma unroll
-      for (int r = 0; r < MR; ++r) tot[c][r] = (kOff != 0.0f ? grp[c][r] - kOff * sx[r] : grp[c][r]) * sc[c];
+      for (int r = 0; r < MR; ++r)
+        tot[c][r] = __builtin_fmaf(kOff != 0.0f ? grp[c][r] - kOff * sx[r] : grp[c][r], sc[c], tot[c][r]);
+    }
   }
 
   // Every wave's tile (rows < M) into LDS as [waves][M][kCols]; each output then adds the waves
-  // in a fixed order.  Thread t owns outputs p = t + i * kSkThreads of the block's M x kCols.
+  // in a fixed order.  Outputs are handled in quads (4 consecutive columns of one row): thread t
+  // owns quads g = t + i * kSkThreads of the block's M x kCols tile.
   const int M = a.M;
   {
     float* rw = red + (size_t)wave * M * kCols;
@@ -236,56 +274,85 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
       if (row < M) {
 #pragma unroll
         for (int c = 0; c < CPL; c += 4)
-          *(float4*)(rw + row * kCols + cg * CPL + c) = make_float4(tot[c][r], tot[c + 1][r], tot[c + 2][r], tot[c + 3][r]);
+          *(f32x4_t*)(rw + row * kCols + cg * CPL + c) = f32x4_t{tot[c][r], tot[c + 1][r], tot[c + 2][r], tot[c + 3][r]};
       }
     }
   }
-  __syncthreads();
-  constexpr int kMaxOut = kSkMaxRows * kCols / kSkThreads;
+  constexpr int kQPR = kCols / 4;                                    // quads per tile row
+  constexpr int kMaxQuads = kSkMaxRows * kQPR / kSkThreads;           // quads per thread (M = 16)
   const int t = threadIdx.x;
-  const int MC = M * kCols;
-  float own[kMaxOut];
-#pragma unroll
-  for (int i = 0; i < kMaxOut; ++i) {
-    const int p = t + i * kSkThreads;
-    float v = 0.0f;
-    if (p < MC) {
-      v = red[p];
-#pragma unroll
-      for (int w = 1; w < kSkWaves; ++w) v += red[w * MC + p];
-    }
-    own[i] = v;
-  }
-  auto finish = [&](int i, float y) {
-    const int p = t + i * kSkThreads;
-    const int m = p / kCols, n = cblk + p % kCols;
-    if (n < a.N) {
-      const float b = a.bias ? load_f(a.bias, n, a.b_dt) : 0.0f;
-      uint16_t o = f32_to_bf16(act_fast(y + b, a.act));
-      if (a.res_op) {  // the folded elementwise op, rounded as the separate op rounds it
-        const float r = load_f(a.res, (size_t)m * a.N + n, a.res_dt), v = bf16_to_f32(o);
-        o = f32_to_bf16(a.res_op == MX_OP_MUL ? mul_rn(v, r) : add_rn(v, r));
-      }
-      a.out[(size_t)m * a.N + n] = o;
-    }
+  const int MC = M * kCols, NQ = M * kQPR;
+  // Epilogue operands of a quad (bias, folded elementwise operand), loaded unconditionally
+  // (clamped into range) so that they travel with the loads they are issued beside.
+  struct QuadOps {
+    SkWord b[4], r[4];
   };
-  if (a.S == 1) {
+  auto quad_ops = [&](int m, int col) {
+    QuadOps q;
+    const int c = min(col, a.N - 4);
 #pragma unroll
-    for (int i = 0; i < kMaxOut; ++i)
-      if (t + i * kSkThreads < MC) finish(i, own[i]);
+    for (int e = 0; e < 4; ++e) {
+      q.b[e] = sk_word(a.bias, c + e, a.b_dt, a.x);
+      q.r[e] = sk_word(a.res_op ? a.res : nullptr, (size_t)m * a.N + c + e, a.res_dt, a.x);
+    }
+    return q;
+  };
+  // bias, activation, bf16, the folded elementwise op (rounded as the separate op rounds it), and
+  // one 8-byte store of the quad.
+  auto finish_quad = [&](int m, int col, f32x4_t y, const QuadOps& q) {
+    if (col >= a.N) return;
+    uint16_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = f32_to_bf16(act_fast(y[e] + sk_value(q.b[e], a.bias, a.b_dt), a.act));
+      if (a.res_op) {
+        const float v = bf16_to_f32(o[e]), r = sk_value(q.r[e], a.res, a.res_dt);
+        o[e] = f32_to_bf16(a.res_op == MX_OP_MUL ? mul_rn(v, r) : add_rn(v, r));
+      }
+    }
+    *(u32x2_v*)(a.out + (size_t)m * a.N + col) = u32x2_v{o[0] | (uint32_t)o[1] << 16, o[2] | (uint32_t)o[3] << 16};
+  };
+
+  if (a.S == 1) {
+    QuadOps ops[kMaxQuads];
+#pragma unroll
+    for (int i = 0; i < kMaxQuads; ++i) {
+      const int g = min(t + i * kSkThreads, NQ - 1);
+      ops[i] = quad_ops(g / kQPR, cblk + 4 * (g % kQPR));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kMaxQuads; ++i) {
+      const int g = t + i * kSkThreads;
+      if (g < NQ) {
+        f32x4_t y = *(const f32x4_t*)(red + 4 * g);
+#pragma unroll
+        for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
+        finish_quad(g / kQPR, cblk + 4 * (g % kQPR), y, ops[i]);
+      }
+    }
     return;
   }
+  __syncthreads();
 
-  // Split K: store this slice's tile (agent-scope relaxed atomics: coherent across the XCDs'
-  // L2s without whole-cache maintenance), wait until the stores have completed, then count the
-  // arrival.  Only the last arriver reads the tiles back.
-  const size_t ss = (size_t)M * a.N;
+  // Split K: store this slice's tile as [slice][M][N] (16-byte stores with the agent-scope
+  // coherence bit sc1: visible across the XCDs' L2s without whole-cache maintenance), wait until
+  // the stores have completed, then count the arrival.  Only the last arriver reads the tiles
+  // back, with loads that carry the same bit.
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      a.partial, (short)0, (int)((size_t)a.S * M * a.N * sizeof(float)), 0x00020000);
+  constexpr int kSc1 = 16;  // cache-policy operand of the buffer intrinsics: sc1
 #pragma unroll
-  for (int i = 0; i < kMaxOut; ++i) {
-    const int p = t + i * kSkThreads;
-    const int m = p / kCols, n = cblk + p % kCols;
-    if (p < MC && n < a.N)
-      __hip_atomic_store(&a.partial[slice * ss + (size_t)m * a.N + n], own[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int i = 0; i < kMaxQuads; ++i) {
+    const int g = t + i * kSkThreads;
+    const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
+    if (g < NQ && col < a.N) {
+      f32x4_t y = *(const f32x4_t*)(red + 4 * g);
+#pragma unroll
+      for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, y), prs,
+                                            (unsigned)(((slice * M + m) * a.N + col) * 4), 0, kSc1);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -297,32 +364,29 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
   }
   __syncthreads();
   if (!s_last) return;
-  // Last arriver: y = sum over slices in slice order.  The loads of kChunk slices of all of this
-  // thread's outputs are issued together (one memory round trip per chunk).
-  constexpr int kChunk = kMaxOut >= 8 ? 4 : 8;
-  float y[kMaxOut];
+  // Last arriver: each quad's S partial tiles, kSl slices per batch of loads (all in flight
+  // together), added in slice order.
+  constexpr int kSl = 16;
+  for (int g = t; g < NQ; g += kSkThreads) {
+    const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
+    const int c = min(col, a.N - 4);
+    f32x4_t y = {0.0f, 0.0f, 0.0f, 0.0f};
+    QuadOps ops;
+    for (int s0 = 0; s0 < a.S; s0 += kSl) {
+      f32x4_t v[kSl];
 #pragma unroll
-  for (int i = 0; i < kMaxOut; ++i) y[i] = 0.0f;
-  for (int s0 = 0; s0 < a.S; s0 += kChunk) {
-    float v[kChunk][kMaxOut];
-#pragma unroll
-    for (int u = 0; u < kChunk; ++u)
-#pragma unroll
-      for (int i = 0; i < kMaxOut; ++i) {
+      for (int u = 0; u < kSl; ++u) {
         const int s = min(s0 + u, a.S - 1);
-        const int p = min(t + i * kSkThreads, MC - 1);
-        const int m = p / kCols, n = min(cblk + p % kCols, a.N - 1);
-        v[u][i] = __hip_atomic_load(&a.partial[s * ss + (size_t)m * a.N + n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v[u] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                               prs, (unsigned)(((s * M + m) * a.N + c) * 4), 0, kSc1));
       }
+      if (s0 == 0) ops = quad_ops(m, col);
 #pragma unroll
-    for (int u = 0; u < kChunk; ++u)
-#pragma unroll
-      for (int i = 0; i < kMaxOut; ++i)
-        if (s0 + u < a.S) y[i] += s0 + u == slice ? own[i] : v[u][i];
+      for (int u = 0; u < kSl; ++u)
+        if (s0 + u < a.S) y += v[u];
+    }
+    finish_quad(m, col, y, ops);
   }
-#pragma unroll
-  for (int i = 0; i < kMaxOut; ++i)
-    if (t + i * kSkThreads < MC) finish(i, y[i]);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -334,47 +398,58 @@ bool qdense_skinny_fits(const QDenseDesc& d) {
   return d.M >= 1 && d.M <= kSkMaxRows && d.x_dt == MX_DTYPE_BFLOAT16 && d.scheme == MX_QUANT_LINEAR && !d.zp &&
          d.block_axis == 0 && d.K >= 32 && d.K % 32 == 0 && G % 32 == 0 && d.N >= 16 &&
          d.N % (dtype_is_packed(d.w_dt) ? 32 : 16) == 0 && d.K < (int64_t)1 << 30 && d.N < (int64_t)1 << 30 &&
-         aligned(d.w, 16) && aligned(d.x, 16) && aligned(d.scale, 16);
+         aligned(d.w, 16) && aligned(d.x, 16) && aligned(d.scale, 16) && aligned(d.out, 8);
 }
 
-// Steps per wave: the largest of 4, 2, 1 that divides both the K steps and the steps of a scale
-// group (a per-output-channel scale is one group spanning K).
-static int skinny_steps_per_wave(const QDenseDesc& d) {
+// Steps per wave T and steps per scale group seen by a wave FL (FL divides T and the steps of a
+// group; a per-output-channel scale is one group spanning K): T = 4 when K/32 allows it and a
+// group holds an even number of steps, else T = FL = 1.  (T = 4 over four 32-row groups would hold
+// four groups' scales in registers.)
+struct SkSteps {
+  int T = 1, FL = 1;
+};
+
+static SkSteps skinny_steps(const QDenseDesc& d) {
   const int64_t ks = d.K / 32;
   const int64_t G = std::min<int64_t>(d.block_size, d.K);
   const int64_t spg = G >= d.K ? ks : G / 32;
-  for (int t : {4, 2})
-    if (ks % t == 0 && spg % t == 0) return t;
-  return 1;
+  SkSteps r;
+  if (ks % 4 == 0 && spg % 2 == 0) {
+    r.T = 4;
+    r.FL = spg % 4 == 0 ? 4 : 2;
+  }
+  return r;
 }
 
-template <int WDT, int T>
-static void launch_t(const SkinnyArgs& ga, int grid, size_t lds, hipStream_t st) {
+template <int WDT, int T, int FL>
+static void launch_fl(const SkinnyArgs& ga, int grid, size_t lds, hipStream_t st) {
   if (ga.M == 1)
-    dispatch(qdense_skinny_kernel<WDT, T, 1>, grid, kSkThreads, lds, st, ga);
+    dispatch(qdense_skinny_kernel<WDT, T, FL, 1>, grid, kSkThreads, lds, st, ga);
   else
-    dispatch(qdense_skinny_kernel<WDT, T, 4>, grid, kSkThreads, lds, st, ga);
+    dispatch(qdense_skinny_kernel<WDT, T, FL, 4>, grid, kSkThreads, lds, st, ga);
 }
 
 template <int WDT>
-static void launch_skinny(const SkinnyArgs& ga, int T, int grid, size_t lds, hipStream_t st) {
-  if (T == 4)
-    launch_t<WDT, 4>(ga, grid, lds, st);
-  else if (T == 2)
-    launch_t<WDT, 2>(ga, grid, lds, st);
-  else
-    launch_t<WDT, 1>(ga, grid, lds, st);
+static void launch_skinny(const SkinnyArgs& ga, SkSteps sp, int grid, size_t lds, hipStream_t st) {
+  if (sp.T == 4) {
+    if (sp.FL == 4)
+      launch_fl<WDT, 4, 4>(ga, grid, lds, st);
+    else
+      launch_fl<WDT, 4, 2>(ga, grid, lds, st);
+  } else {
+    launch_fl<WDT, 1, 1>(ga, grid, lds, st);
+  }
 }
 
 int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   const bool i4 = dtype_is_packed(d.w_dt);
   const int64_t cols = i4 ? 256 : 128;
   const int64_t nb = (d.N + cols - 1) / cols;
-  const int T = skinny_steps_per_wave(d);
-  const int64_t chunks = d.K / 32 / T;  // wave-sized pieces of one column block
+  const SkSteps sp = skinny_steps(d);
+  const int64_t chunks = d.K / 32 / sp.T;  // wave-sized pieces of one column block
   const int64_t S = (chunks + kSkWaves - 1) / kSkWaves;
   const size_t counter_bytes = 64 * 1024;
-  if ((size_t)nb * 4 > counter_bytes || nb * S > (int64_t)1 << 30)
+  if ((size_t)nb * 4 > counter_bytes || nb * S > (int64_t)1 << 30 || S * d.M * d.N * 4 >= (int64_t)1 << 31)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: N=%lld too large for the skinny path", (long long)d.N);
   SkinnyArgs ga;
   ga.x = (const uint16_t*)d.x;
@@ -402,14 +477,15 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.res_dt = d.res_dt;
   ga.res_op = d.res_op;
   const int grid = (int)(nb * S);
+  // LDS: the waves' tiles [waves][M][cols].
   const size_t lds = (size_t)kSkWaves * d.M * cols * sizeof(float);
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     switch (d.w_dt) {
-      case MX_DTYPE_INT4: launch_skinny<MX_DTYPE_INT4>(ga, T, grid, lds, st); break;
-      case MX_DTYPE_UINT4: launch_skinny<MX_DTYPE_UINT4>(ga, T, grid, lds, st); break;
-      case MX_DTYPE_INT8: launch_skinny<MX_DTYPE_INT8>(ga, T, grid, lds, st); break;
-      default: launch_skinny<MX_DTYPE_UINT8>(ga, T, grid, lds, st); break;
+      case MX_DTYPE_INT4: launch_skinny<MX_DTYPE_INT4>(ga, sp, grid, lds, st); break;
+      case MX_DTYPE_UINT4: launch_skinny<MX_DTYPE_UINT4>(ga, sp, grid, lds, st); break;
+      case MX_DTYPE_INT8: launch_skinny<MX_DTYPE_INT8>(ga, sp, grid, lds, st); break;
+      default: launch_skinny<MX_DTYPE_UINT8>(ga, sp, grid, lds, st); break;
     }
   });
 }
