@@ -8,29 +8,29 @@
 //
 // Tiling.  A workgroup (8 waves, two per SIMD) computes a 256 x 128 output tile; wave w owns
 // rows [64 wr, 64 wr + 64) x columns [64 wc, 64 wc + 64) with wr = w % 4, wc = w / 4.  K advances
-// in blocks of 64 (two 32-row steps of v_mfma_f32_16x16x32_bf16).
-//   - x: a 3-stage LDS ring of [256 rows][64 k] bf16 tiles filled by direct global->LDS loads
-//     (16 bytes per lane) issued two blocks ahead; 16-byte chunks are XOR-swizzled within each
-//     row by (row >> 1) & 7 so that an MFMA operand read (16 rows) hits distinct banks.
-//   - w: each thread loads 4 rows x 4 columns of int8 per block into registers (two blocks
-//     ahead; a wave's load covers 2 rows x 128 contiguous bytes), converts them exactly to bf16
-//     (|w| < 256 has at most 8 significant bits) and writes them transposed into a bf16 tile
-//     Bt[128 columns][64 k], double-buffered, whose 16-byte k-chunks are XOR-swizzled by
-//     (column >> 2) & 7 (conflict-free B-operand reads: 8 consecutive k of one column).
-//     Block kb + 1 is dequantised between the two MFMA steps of block kb, so the weights are
-//     converted once per workgroup and the conversion overlaps the matrix cores.
-// One barrier per K block publishes the next Bt buffer and retires the reads of the current ring
-// stage, which is then refilled.  Every load is issued unconditionally (block indices past the
-// end are clamped), so the number of loads in flight is the same in every iteration and the
-// explicit vmcnt waits are exact.  Lane (cg = lane % 16, kq = lane / 16) ends with rows 4*kq + r
-// of each 16-row block and the 4 consecutive columns 4*cg .. 4*cg + 3 of its wave's 64; the
-// epilogue applies scale, bias and activation and writes 8-byte bf16 runs.
+// in blocks of 64 (two 32-row steps of v_mfma_f32_16x16x32_bf16).  LDS holds two buffers of
+//   - x: [256 rows][64 k] bf16; 16-byte k-chunks XOR-swizzled within each row by (row >> 1) & 7
+//     so that an MFMA operand read (16 rows) hits distinct banks;
+//   - Bt: [128 columns][64 k] bf16, the int8 weights converted exactly to bf16 (|w| < 256 has at
+//     most 8 significant bits) and transposed.  Column c is stored in row p = c ^ ((c >> 2) & 1)
+//     and its 16-byte k-chunks are XOR-swizzled by (p >> 3) & 7: the 16 lanes of a B-operand read
+//     (columns 4 apart) then cover both halves of the banks and 8 distinct chunks in each.
+// Block kb runs its MFMAs from buffer kb % 2 while the workgroup's loads of block kb + 4 travel
+// into registers (four blocks of lead cover an L2 miss) and block kb + 1, loaded three blocks
+// earlier, is written into the other buffer: each thread loads 4 x 16 bytes of x (8 threads per
+// 128-byte row segment) and 4 rows x 4 columns of int8 weights (32 threads per 128-byte row
+// segment) per block.  One barrier per block publishes the next buffers and retires the reads
+// of the current ones; it sits between the block's two steps, so that the next block's step-0
+// operand reads travel under step 1's MFMAs.  Every access is compiler-visible (the compiler
+// places the waits), and sched_group_barrier interleaves the memory instructions one per MFMA:
+// issuing a global load or an LDS access can stall the wave (the CU's vector-memory path takes
+// 40 KB per block, and LDS writes run at about 90 bytes/clock per CU), and a stall that overlaps
+// an MFMA in flight costs nothing.  Loads past the last block re-read it (clamped index).
+// Lane (cg = lane % 16, kq = lane / 16) ends with rows 4*kq + r of each 16-row block and the 4
+// consecutive columns 4*cg .. 4*cg + 3 of its wave's 64; the epilogue applies scale, bias and
+// activation and writes 8-byte bf16 runs.
 // Tile order: every XCD (workgroups are dispatched round-robin over the 8) takes a 2 x 16 block
 // of tiles, so its L2 serves the x rows and w columns they share.
-//
-// The LDS accesses are inline assembly: LDS reads or writes written in C++ after the direct
-// global->LDS loads would make the compiler wait for every outstanding load (vmcnt(0)) first,
-// emptying the prefetch ring.  The asm blocks wait for their own results (lgkmcnt).
 #include <algorithm>
 #include <type_traits>
 
@@ -44,16 +44,15 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-typedef __attribute__((address_space(1))) void* gbl_void_ptr;
-
-constexpr int kBM = 256, kBN = 128, kBK = 64, kWaves = 8, kThreads = 64 * kWaves, kStages = 3;
-constexpr int kABytes = kBM * kBK * 2;              // 32 KB per ring stage
-constexpr int kBtBytes = kBN * kBK * 2;             // 16 KB per Bt buffer
-constexpr int kLds = kStages * kABytes + 2 * kBtBytes;
-constexpr int kAInstr = kABytes / (kWaves * 1024);  // direct loads per wave per stage
-constexpr int kWLoads = 4;                          // w loads per thread per block
-static_assert(kAInstr * kWaves * 1024 == kABytes, "x load split");
+constexpr int kBM = 256, kBN = 128, kBK = 64, kWaves = 8, kThreads = 64 * kWaves;
+constexpr int kABytes = kBM * kBK * 2;   // 32 KB per x buffer
+constexpr int kBtBytes = kBN * kBK * 2;  // 16 KB per Bt buffer
+constexpr int kLds = 2 * kABytes + 2 * kBtBytes;
+constexpr int kXLoads = kABytes / (kThreads * 16);  // 16-byte x loads per thread per block
+constexpr int kWLoads = 4;                           // w loads (4 bytes) per thread per block
+constexpr int kPf = 4;                               // blocks loaded ahead into registers
+constexpr int kUnroll = 4;                           // multiple of kPf and of the 2 LDS buffers
+static_assert(kXLoads * kThreads * 16 == kABytes, "x load split");
 static_assert(kBK * kBN == 16 * kThreads, "conversion: 16 weights per thread");
 
 struct GemmArgs {
@@ -65,59 +64,18 @@ struct GemmArgs {
   int M, K, N, s_dt, b_dt, act, tiles_n, grouped;
 };
 
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-  __builtin_amdgcn_global_load_lds((gbl_void_ptr)const_cast<void*>(src), (lds_void_ptr)(uintptr_t)lds, 16, 0, 0);
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
 __device__ __forceinline__ f32x4_t mfma(const u32x4_v& a, const u32x4_v& b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
                                                  0, 0, 0);
 }
 
-// Four bf16 k-values of each of four consecutive columns of Bt (rows 128 bytes apart).
-__device__ __forceinline__ void write_bt4(uint32_t addr, const u32x2_v (&v)[4]) {
-  asm volatile(
-      "ds_write_b64 %0, %1 offset:0\n\t"
-      "ds_write_b64 %0, %2 offset:128\n\t"
-      "ds_write_b64 %0, %3 offset:256\n\t"
-      "ds_write_b64 %0, %4 offset:384\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      :
-      : "v"(addr), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3])
-      : "memory");
+// Workgroup barrier ordering LDS only: waits for this wave's LDS accesses, not for its global
+// loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
-
-// One K step's operands: the wave's 4 x-row blocks (16 bytes each, 2 KB apart) and its 4
-// Bt-column blocks (16 bytes each, 128 bytes apart).
-__device__ __forceinline__ void read_step(uint32_t aa, uint32_t ba, u32x4_v (&A)[4], u32x4_v (&B)[4]) {
-  asm volatile(
-      "ds_read_b128 %0, %8 offset:0\n\t"
-      "ds_read_b128 %1, %8 offset:2048\n\t"
-      "ds_read_b128 %2, %8 offset:4096\n\t"
-      "ds_read_b128 %3, %8 offset:6144\n\t"
-      "ds_read_b128 %4, %9 offset:0\n\t"
-      "ds_read_b128 %5, %9 offset:128\n\t"
-      "ds_read_b128 %6, %9 offset:256\n\t"
-      "ds_read_b128 %7, %9 offset:384\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(A[0]), "=&v"(A[1]), "=&v"(A[2]), "=&v"(A[3]), "=&v"(B[0]), "=&v"(B[1]), "=&v"(B[2]), "=&v"(B[3])
-      : "v"(aa), "v"(ba)
-      : "memory");
-}
-
-// Workgroup barrier.  The LDS accesses around it are asm blocks that have waited for their own
-// completion, so the barrier alone orders them.
-__device__ __forceinline__ void barrier() { __builtin_amdgcn_s_barrier(); }
 
 // act(v * s + b) rounded to bf16, for a compile-time activation.
 template <int ACT>
@@ -150,7 +108,6 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
 
 template <int WDT>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   // Tile order: consecutive work items go to one XCD (workgroups are dispatched round-robin over
   // the 8); with whole 2 x 16 tile groups, 32 consecutive items form one group.
   const int total = gridDim.x;
@@ -172,38 +129,46 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   const int KB = a.K / kBK;
   const size_t N = (size_t)a.N;
 
-  // x direct loads: this wave fills stage chunks q = 64*(4*wave + i) + lane; chunk q holds row
-  // r = q / 8, k-chunk (q % 8) ^ ((r >> 1) & 7).  Rows past M read row M-1.
-  const uint16_t* asrc[kAInstr];
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kABytes];
+  __shared__ __attribute__((aligned(16))) uint8_t bt[2][kBtBytes];
+
+  // x: thread t loads chunks q = t + kThreads * i: row q / 8, k-chunk q % 8 (16 bytes), stored at
+  // chunk (q % 8) ^ ((row >> 1) & 7) of the row.  Rows past M read row M-1.
+  const int t = threadIdx.x;
+  const uint16_t* xsrc[kXLoads];
+  uint32_t xdst[kXLoads];
 #pragma unroll
-  for (int i = 0; i < kAInstr; ++i) {
-    const int q = 64 * (kAInstr * wave + i) + lane;
-    const int r = q >> 3, c = (q & 7) ^ ((r >> 1) & 7);
-    asrc[i] = a.x + (size_t)min(m0 + r, a.M - 1) * a.K + 8 * c;
+  for (int i = 0; i < kXLoads; ++i) {
+    const int q = t + kThreads * i;
+    const int r = q >> 3, c = q & 7;
+    xsrc[i] = a.x + (size_t)min(m0 + r, a.M - 1) * a.K + 8 * c;
+    xdst[i] = (uint32_t)(r * (kBK * 2) + ((c ^ ((r >> 1) & 7)) << 4));
   }
-  const uint32_t smem_base = lds_addr(smem);
-  const uint32_t bt_base = smem_base + kStages * kABytes;
-  auto issue_x = [&](int kb) {
-    const uint32_t st = smem_base + (uint32_t)((kb % kStages) * kABytes);
+  auto load_x = [&](int kb, u32x4_v (&dst)[kXLoads]) {
     kb = min(kb, KB - 1);
 #pragma unroll
-    for (int i = 0; i < kAInstr; ++i) dma16(asrc[i] + kb * kBK, st + (uint32_t)((kAInstr * wave + i) * 1024));
+    for (int i = 0; i < kXLoads; ++i) dst[i] = *(const u32x4_v*)(xsrc[i] + (size_t)kb * kBK);
+  };
+  auto store_x = [&](const u32x4_v (&v)[kXLoads], int buf) {
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) *(u32x4_v*)(&xs[buf][xdst[i]]) = v[i];
   };
   // w: thread t converts columns 4*cq .. 4*cq + 3 and rows 4*j .. 4*j + 3 of each block; the 32
   // threads of a j read 128 contiguous bytes of a row.  Columns past N read column 0 (their
   // outputs are not stored).
-  const int t = threadIdx.x, cq = t & 31, j = t >> 5;
+  const int cq = t & 31, j = t >> 5;
   const int wcol = n0 + 4 * cq + 4 <= a.N ? n0 + 4 * cq : 0;
   const uint8_t* wsrc = a.w + (size_t)(4 * j) * N + wcol;
-  const uint32_t cv_addr = bt_base + (uint32_t)(4 * cq * (kBK * 2) + (((j >> 1) ^ (cq & 7)) << 4) + ((j & 1) << 3));
+  // Column 4*cq + c lives in Bt row (4*cq + c) ^ (cq & 1), k-chunk j / 2 swizzled by (cq / 2) & 7.
+  const uint32_t cv_off = (uint32_t)((((j >> 1) ^ ((cq >> 1) & 7)) << 4) + ((j & 1) << 3));
   auto load_w = [&](int kb, uint32_t (&dst)[kWLoads]) {
     kb = min(kb, KB - 1);
 #pragma unroll
     for (int e = 0; e < kWLoads; ++e)
       dst[e] = __builtin_nontemporal_load((const uint32_t*)(wsrc + (size_t)(kb * kBK + e) * N));
   };
-  auto convert = [&](const uint32_t (&w4)[kWLoads], int buf) {
-    u32x2_v v[4];
+  // Four bf16 k-values of each of four consecutive columns (Bt rows 128 bytes apart).
+  auto store_w = [&](const uint32_t (&w4)[kWLoads], int buf) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float f[4];
@@ -214,10 +179,10 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
         else
           f[e] = (float)(uint8_t)(w4[e] >> (8 * c));
       }
-      v[c] = u32x2_v{__builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u),
-                     __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u)};
+      *(u32x2_v*)(&bt[buf][cv_off + (uint32_t)((4 * cq + (c ^ (cq & 1))) * (kBK * 2))]) =
+          u32x2_v{__builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u),
+                  __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u)};
     }
-    write_bt4(cv_addr + (uint32_t)(buf * kBtBytes), v);
   };
 
   f32x4_t acc[4][4];
@@ -226,60 +191,98 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // MFMA operand reads: x row 64*wr + cg of the first row block; Bt column 64*wc + 4*cg.
+  // MFMA operands of one 32-row step: x row 64*wr + 16*rb + cg, Bt column 64*wc + 4*cg + c (Bt
+  // row 64*wc + 4*cg + (c ^ (cg & 1))).
   const uint32_t a_row = (uint32_t)((64 * wr + cg) * (kBK * 2));
-  const uint32_t b_col = bt_base + (uint32_t)((64 * wc + 4 * cg) * (kBK * 2));
-  auto mma_step = [&](int kb, int buf, int sub) {
-    const uint32_t sb = smem_base + (uint32_t)((kb % kStages) * kABytes);
+  const uint32_t b_col = (uint32_t)((64 * wc + 4 * cg) * (kBK * 2));
+  const int b_par = cg & 1;
+  // Operands of one 32-row step (sub = 0, 1 of a block) from LDS buffer buf, and its 16 MFMAs.
+  auto read_step = [&](int buf, int sub, u32x4_v (&A)[4], u32x4_v (&B)[4]) {
     const int kc = 4 * sub + kq;  // 16-byte k-chunk of this lane
-    const uint32_t aa = sb + a_row + (uint32_t)((kc ^ (cg >> 1)) << 4);
-    const uint32_t ba = b_col + (uint32_t)(buf * kBtBytes) + (uint32_t)((kc ^ (cg & 7)) << 4);
-    u32x4_v A[4], B[4];
-    read_step(aa, ba, A, B);
+    const uint8_t* ap = &xs[buf][a_row + ((kc ^ (cg >> 1)) << 4)];
+    const uint8_t* bp = &bt[buf][b_col + ((kc ^ ((cg >> 1) & 7)) << 4)];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) A[rb] = *(const u32x4_v*)(ap + rb * 16 * (kBK * 2));
+#pragma unroll
+    for (int c = 0; c < 4; ++c) B[c] = *(const u32x4_v*)(bp + (c ^ b_par) * (kBK * 2));
+  };
+  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[4]) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc[rb][c] = mfma(A[rb], B[c], acc[rb][c]);
   };
 
-  // Loads in flight, in issue order, at the end of block kb (before its wait): x block kb + 1,
-  // w block kb + 2, x block kb + 2, w block kb + 3.  Block kb + 1's x is complete once only the
-  // three newer groups are outstanding.
-  constexpr int kWaitX = kWLoads + kAInstr + kWLoads;
-  uint32_t wv[2][kWLoads];  // [ring slot][row]: w of blocks kb + 1 and kb + 2
-  // One K block; S = kb % 2 (compile-time, so the w ring is indexed statically).  On entry Bt
-  // buffer S holds block kb, wv[S ^ 1] holds block kb + 1's int8 weights and x block kb is in its
-  // ring stage.
-  auto block = [&](int kb, auto slot) {
-    constexpr int S = decltype(slot)::value;
-    mma_step(kb, S, 0);
+  // Register slots hold the next kPf blocks' x and w: block kb's slot is free once block kb
+  // is in LDS (written during block kb - 1), so block kb refills it with block kb + kPf and
+  // writes block kb + 1 into the other LDS buffer.  The order keeps the matrix cores fed while
+  // LDS traffic is in flight: on entry step 0's operands of block kb are in registers (A0, B0);
+  // step 1's reads and block kb + 1's writes are issued before step 0's MFMAs, and after the
+  // barrier that publishes block kb + 1, its step-0 reads are issued before step 1's MFMAs.
+  // (sched_barrier keeps the compiler from regrouping the phases.)
+  u32x4_v xr[kPf][kXLoads];
+  uint32_t wr4[kPf][kWLoads];
+  u32x4_v A0[4], B0[4], A1[4], B1[4];
+  auto block = [&](int kb, auto step) {
+    constexpr int U = decltype(step)::value;  // kb % kUnroll
+    constexpr int S = U % kPf, S1 = (U + 1) % kPf, B = U % 2;
+    // Step 0: its MFMAs interleaved with step 1's operand reads, then with the conversion and
+    // LDS writes of block kb + 1, so that every issue stall of a memory instruction overlaps an
+    // MFMA in flight.
+    read_step(B, 1, A1, B1);
+    store_x(xr[S1], B ^ 1);
+    store_w(wr4[S1], B ^ 1);
+    mma_step(A0, B0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    }
     __builtin_amdgcn_sched_barrier(0);
-    convert(wv[S ^ 1], S ^ 1);
-    load_w(kb + 3, wv[S ^ 1]);
+    lds_barrier();
+    // Step 1: its MFMAs interleaved with block kb + 1's step-0 reads and the global loads of
+    // block kb + kPf.
+    read_step(B ^ 1, 0, A0, B0);
+    load_x(kb + kPf, xr[S]);
+    load_w(kb + kPf, wr4[S]);
+    mma_step(A1, B1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    }
     __builtin_amdgcn_sched_barrier(0);
-    mma_step(kb, S, 1);
-    wait_vmcnt<kWaitX>();
-    barrier();  // Bt buffer S ^ 1 published; every read of x stage kb and Bt buffer S retired
-    issue_x(kb + 3);
   };
+  auto blocks = [&](int kb, int n, auto... steps) { ((steps.value < n ? block(kb + steps.value, steps) : void()), ...); };
 
-  issue_x(0);
-  load_w(0, wv[0]);
-  issue_x(1);
-  load_w(1, wv[1]);
-  issue_x(2);
-  convert(wv[0], 0);  // waits (compiler) for block 0's w
-  load_w(2, wv[0]);
-  // In flight now: x0, x1, w1, x2, w2 (w0 done); x0 complete once x1, w1, x2, w2 may remain.
-  wait_vmcnt<kAInstr + kWLoads + kAInstr + kWLoads>();
-  barrier();
-  int kb = 0;
-  for (; kb + 1 < KB; kb += 2) {
-    block(kb, std::integral_constant<int, 0>{});
-    block(kb + 1, std::integral_constant<int, 1>{});
+#pragma unroll
+  for (int p = 0; p < kPf; ++p) {
+    load_x(p, xr[p]);
+    load_w(p, wr4[p]);
   }
-  if (kb < KB) block(kb, std::integral_constant<int, 0>{});
-  wait_vmcnt<0>();  // drain the clamped prefetches before the workgroup's LDS is released
+  store_x(xr[0], 0);
+  store_w(wr4[0], 0);
+  lds_barrier();
+  read_step(0, 0, A0, B0);
+  int kb = 0;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  static_assert(kUnroll == 4, "unrolled steps");
+  for (; kb + kUnroll <= KB; kb += kUnroll) blocks(kb, kUnroll, I0{}, I1{}, I2{}, I3{});
+  blocks(kb, KB - kb, I0{}, I1{}, I2{});
 
   // Epilogue: y = act(acc * s[n] + bias[n]) for this lane's 4 columns.
   const int ncol = n0 + 64 * wc + 4 * cg;
@@ -334,9 +337,9 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     if (d.w_dt == MX_DTYPE_INT8)
-      dispatch(qdense_gemm_kernel<MX_DTYPE_INT8>, grid, kThreads, kLds, st, ga);
+      dispatch(qdense_gemm_kernel<MX_DTYPE_INT8>, grid, kThreads, 0, st, ga);
     else
-      dispatch(qdense_gemm_kernel<MX_DTYPE_UINT8>, grid, kThreads, kLds, st, ga);
+      dispatch(qdense_gemm_kernel<MX_DTYPE_UINT8>, grid, kThreads, 0, st, ga);
   });
 }
 
