@@ -4,7 +4,7 @@ Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import 
 and only as the checker (or the timed CPU baseline), never as a product path.
 
 It loads oracle/_build/liboracle.so (a plain-C restatement of the reference's arithmetic,
-qdense_ref.c) and provides numpy helpers: seeded generators for the BASELINE configurations, the
+qdense_ref.c and ggml_ref.c) and provides numpy helpers: seeded generators for the BASELINE configurations, the
 reference packing of 4-bit weights, bf16 rounding, and brute-force numpy restatements of the
 DotGeneral output layout (shapeinference/dotgeneral.go:16-152) for small cases.
 """
@@ -21,6 +21,7 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 SRC = HERE / "qdense_ref.c"
+SRC_GGML = HERE / "ggml_ref.c"
 LIB = HERE / "_build" / "liboracle.so"
 
 DT_INT8, DT_UINT8, DT_INT4, DT_UINT4 = 2, 6, 21, 22
@@ -34,7 +35,7 @@ def build() -> Path:
     LIB.parent.mkdir(parents=True, exist_ok=True)
     tmp = LIB.with_suffix(".so.tmp")
     cmd = ["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
-           "-o", str(tmp), str(SRC), "-lm"]
+           "-o", str(tmp), str(SRC), str(SRC_GGML), "-lm"]
     subprocess.run(cmd, check=True, capture_output=True, text=True)
     os.replace(tmp, LIB)
     return LIB
@@ -68,6 +69,18 @@ def lib() -> C.CDLL:
                                                                           C.c_int64, C.c_int64]
         L.oracle_qdense_abs.argtypes = common + [dp] + [C.c_int64] * 3 + [C.c_int, C.c_int, C.c_int64,
                                                                           C.c_int64, C.c_int64]
+        u8p = C.c_void_p
+        L.oracle_f16_to_f32.argtypes = [C.c_uint16]
+        L.oracle_f16_to_f32.restype = C.c_float
+        L.oracle_f16_to_f32_array.argtypes = [C.c_void_p, C.c_size_t, fp]
+        L.oracle_ggml_values_per_block.argtypes = [C.c_int]
+        L.oracle_ggml_bytes_per_block.argtypes = [C.c_int]
+        L.oracle_ggml_dequant_row.argtypes = [C.c_int, u8p, C.c_int64, fp]
+        L.oracle_ggml_dense.argtypes = [fp, u8p, C.c_int, fp, fp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int]
+        L.oracle_ggml_dense_f64.argtypes = [fp, u8p, C.c_int, fp, dp, dp, C.c_int64, C.c_int64, C.c_int64,
+                                            C.c_int64]
+        L.oracle_ggml_embedding.argtypes = [u8p, C.c_int64, C.c_int64, C.c_int, C.c_void_p, C.c_int64, fp]
+        L.oracle_ggml_embedding.restype = C.c_int64
         _lib = L
     return _lib
 
@@ -285,3 +298,84 @@ def dot_general(lhs: np.ndarray, lc, lb, rhs: np.ndarray, rc, rb) -> np.ndarray:
     R = R.reshape(Bn, Kn, Nn)
     out = np.matmul(L, R)  # float64
     return out.reshape(bshape + mshape + nshape)
+
+
+# ---------------------------------------------------------------------------------------------
+# GGML block formats (quantizeddense_ggml.go, quantizeddense.go:455-499).
+# ---------------------------------------------------------------------------------------------
+GGML_Q4_0, GGML_Q8_0, GGML_IQ4_NL, GGML_Q4_K, GGML_Q6_K = 0, 1, 2, 5, 7
+GGML_TYPES = (GGML_Q4_0, GGML_Q8_0, GGML_IQ4_NL, GGML_Q4_K, GGML_Q6_K)
+
+
+def ggml_block(t: int):
+    """(values per block, bytes per block) of a GGML type (fused_ops.go:148-177)."""
+    return lib().oracle_ggml_values_per_block(t), lib().oracle_ggml_bytes_per_block(t)
+
+
+def f16_to_f32(h) -> np.ndarray:
+    a = np.ascontiguousarray(np.asarray(h, dtype=np.uint16))
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().oracle_f16_to_f32_array(a.ctypes.data, a.size, out.ctypes.data_as(C.POINTER(C.c_float)))
+    return out
+
+
+def ggml_dequant(t: int, rows) -> np.ndarray:
+    """[R, bytesPerRow] uint8 -> [R, K] float32 (dequantXXXRow per row)."""
+    r = np.ascontiguousarray(np.asarray(rows, dtype=np.uint8))
+    R, bpr = r.shape
+    vpb, bpb = ggml_block(t)
+    K = bpr // bpb * vpb
+    out = np.empty((R, K), dtype=np.float32)
+    for i in range(R):
+        rc = lib().oracle_ggml_dequant_row(t, r[i].ctypes.data, bpr,
+                                           out[i].ctypes.data_as(C.POINTER(C.c_float)))
+        if rc != 0:
+            raise ValueError(f"unsupported GGML type {t}")
+    return out
+
+
+def ggml_dense(x, w, t: int, bias=None, act_: int = ACT_NONE) -> np.ndarray:
+    """Reference-order f32 result of FusedQuantizedDense(GGML): x [M, K] f32, w [N, bytesPerRow]."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    w = np.ascontiguousarray(np.asarray(w, dtype=np.uint8))
+    M, K = x.shape
+    N, bpr = w.shape
+    out = np.empty((M, N), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(np.asarray(bias, dtype=np.float32))
+    fp = C.POINTER(C.c_float)
+    rc = lib().oracle_ggml_dense(x.ctypes.data_as(fp), w.ctypes.data, t, None if b is None else b.ctypes.data_as(fp),
+                                 out.ctypes.data_as(fp), M, K, N, bpr, act_)
+    if rc != 0:
+        raise ValueError(f"oracle_ggml_dense failed ({rc})")
+    return out
+
+
+def ggml_dense_f64(x, w, t: int, bias=None):
+    """(exact f64 value, sum of |terms|) of x @ dequant(w)^T + bias."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    w = np.ascontiguousarray(np.asarray(w, dtype=np.uint8))
+    M, K = x.shape
+    N, bpr = w.shape
+    out = np.empty((M, N), dtype=np.float64)
+    ab = np.empty((M, N), dtype=np.float64)
+    b = None if bias is None else np.ascontiguousarray(np.asarray(bias, dtype=np.float32))
+    fp, dp = C.POINTER(C.c_float), C.POINTER(C.c_double)
+    rc = lib().oracle_ggml_dense_f64(x.ctypes.data_as(fp), w.ctypes.data, t, None if b is None else b.ctypes.data_as(fp),
+                                     out.ctypes.data_as(dp), ab.ctypes.data_as(dp), M, K, N, bpr)
+    if rc != 0:
+        raise ValueError(f"oracle_ggml_dense_f64 failed ({rc})")
+    return out, ab
+
+
+def ggml_embedding(data, t: int, idx) -> np.ndarray:
+    """QuantizedEmbeddingLookup: data [vocab, bytesPerRow], idx int (any shape) -> [n, K] f32."""
+    d = np.ascontiguousarray(np.asarray(data, dtype=np.uint8))
+    i = np.ascontiguousarray(np.asarray(idx, dtype=np.int64).ravel())
+    vpb, bpb = ggml_block(t)
+    K = d.shape[1] // bpb * vpb
+    out = np.empty((i.size, K), dtype=np.float32)
+    rc = lib().oracle_ggml_embedding(d.ctypes.data, d.shape[0], d.shape[1], t, i.ctypes.data, i.size,
+                                     out.ctypes.data_as(C.POINTER(C.c_float)))
+    if rc != 0:
+        raise IndexError(f"index {int(i[rc - 1])} out of range [0, {d.shape[0]})")
+    return out
