@@ -12,6 +12,8 @@ from .backend import (  # noqa: F401
     ActivationType, Backend, Buffer, Builder, Capabilities, ComputeError, DotGeneralConfig, ErrFinalized,
     ErrNoDevice, ErrNotImplemented, Executable, Function, IsNotImplemented, NF4LookupTable, New, OpType,
     QuantGGML, QuantLinear, QuantNF4, Quantization, QuantizationScheme, Value,
+    GGMLQuantType, GGMLQ4_0, GGMLQ8_0, GGMLIQ4NL, GGMLQ2_K, GGMLQ3_K, GGMLQ4_K, GGMLQ5_K, GGMLQ6_K,
+    IQ4NLLookupTable, ggml_bytes_per_block, ggml_values_per_block,
 )
 
 BackendName = "mi355x"

@@ -57,6 +57,20 @@ class mx_qdense_args(C.Structure):
         ("block_axis", C.c_int32),
         ("block_size", C.c_int32),
         ("activation", C.c_int32),
+        ("ggml_type", C.c_int32),
+    ]
+
+
+class mx_qembed_args(C.Structure):
+    _fields_ = [
+        ("data", C.c_void_p),
+        ("indices", C.c_void_p),
+        ("out", C.c_void_p),
+        ("vocab", C.c_int64),
+        ("bytes_per_row", C.c_int64),
+        ("n", C.c_int64),
+        ("index_dtype", C.c_int32),
+        ("ggml_type", C.c_int32),
     ]
 
 
@@ -106,6 +120,7 @@ SIGNATURES = {
     "mx_fn_shape": [_P, _VAL, _SHP],
     "mx_fn_return": [_P, _VALP, _I],
     "mx_fn_fused_quantized_dense": [_P, _VAL, _VAL, _VAL, C.POINTER(mx_quantization), _I, _VALP],
+    "mx_fn_quantized_embedding_lookup": [_P, _VAL, _VAL, C.POINTER(mx_quantization), _VALP],
     "mx_fn_dot_general": [_P, _VAL, _I32P, _I, _I32P, _I, _VAL, _I32P, _I, _I32P, _I, _I, _I, _VALP],
     "mx_fn_fused_dense": [_P, _VAL, _VAL, _VAL, _I, _VALP],
     "mx_fn_fused_gelu": [_P, _VAL, _I, _VALP],
@@ -129,6 +144,7 @@ SIGNATURES = {
     "mx_exec_describe": [_P, C.c_char_p, _SZ],
     "mx_qdense": [_P, C.POINTER(mx_qdense_args)],
     "mx_qdense_plan": [_P, C.POINTER(mx_qdense_args), C.c_char_p, _SZ],
+    "mx_quantized_embedding_lookup": [_P, C.POINTER(mx_qembed_args)],
 }
 
 _RESTYPES = {"mx_last_error": C.c_char_p}

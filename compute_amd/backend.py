@@ -128,6 +128,37 @@ NF4LookupTable = np.array([
 ], dtype=np.float32)  # fused_ops.go:116-121
 
 
+class GGMLQuantType(enum.IntEnum):
+    """compute.GGMLQuantType (fused_ops.go:134-146)."""
+
+    GGMLQ4_0 = 0
+    GGMLQ8_0 = 1
+    GGMLIQ4NL = 2
+    GGMLQ2_K = 3
+    GGMLQ3_K = 4
+    GGMLQ4_K = 5
+    GGMLQ5_K = 6
+    GGMLQ6_K = 7
+
+
+GGMLQ4_0, GGMLQ8_0, GGMLIQ4NL, GGMLQ2_K, GGMLQ3_K, GGMLQ4_K, GGMLQ5_K, GGMLQ6_K = GGMLQuantType
+
+IQ4NLLookupTable = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113],
+                            dtype=np.float32)  # fused_ops.go:127-130
+
+
+def ggml_values_per_block(t: int) -> int:
+    """GGMLQuantType.ValuesPerBlock (fused_ops.go:148-156)."""
+    return {GGMLQ4_0: 32, GGMLQ8_0: 32, GGMLIQ4NL: 32, GGMLQ2_K: 256, GGMLQ3_K: 256, GGMLQ4_K: 256,
+            GGMLQ5_K: 256, GGMLQ6_K: 256}.get(int(t), 0)
+
+
+def ggml_bytes_per_block(t: int) -> int:
+    """GGMLQuantType.BytesPerBlock (fused_ops.go:158-177)."""
+    return {GGMLQ4_0: 18, GGMLQ8_0: 34, GGMLIQ4NL: 18, GGMLQ2_K: 84, GGMLQ3_K: 110, GGMLQ4_K: 144,
+            GGMLQ5_K: 176, GGMLQ6_K: 210}.get(int(t), 0)
+
+
 @dataclass
 class Quantization:
     """compute.Quantization (fused_ops.go:204-234).
@@ -292,6 +323,9 @@ class Backend:
         buf = C.create_string_buffer(128)
         _check(self._lib.mx_qdense_plan(self._h, C.byref(args), buf, len(buf)))
         return buf.value.decode()
+
+    def QEmbed(self, args: _lib.mx_qembed_args) -> None:
+        _check(self._lib.mx_quantized_embedding_lookup(self._h, C.byref(args)))
 
     # -- profiling / debugging ------------------------------------------------------------
     def SetProfiling(self, enabled: bool) -> None:
@@ -485,6 +519,14 @@ class Function:
                                   int(q.BlockSize), int(q.GGMLType))
         return self._out(self._lib.mx_fn_fused_quantized_dense, int(x), int(weights), int(bias or 0), C.byref(cq),
                          int(activation))
+
+    def QuantizedEmbeddingLookup(self, data: Value, indices: Value, dataQuantization: Quantization) -> Value:
+        q = dataQuantization
+        if q is None:
+            raise ComputeError(_lib.MX_ERR_INVALID, "QuantizedEmbeddingLookup: quantization is nil")
+        cq = _lib.mx_quantization(int(q.Scheme), int(q.Scale or 0), int(q.ZeroPoint or 0), int(q.BlockAxis),
+                                  int(q.BlockSize), int(q.GGMLType))
+        return self._out(self._lib.mx_fn_quantized_embedding_lookup, int(data), int(indices), C.byref(cq))
 
     def FusedDense(self, x: Value, weight: Value, bias: Optional[Value], activation=ActivationNone) -> Value:
         return self._out(self._lib.mx_fn_fused_dense, int(x), int(weight), int(bias or 0), int(activation))

@@ -1,0 +1,498 @@
+// GGML block formats on gfx950: FusedQuantizedDense with weights [N, bytesPerRow] in Q4_0, Q8_0,
+// IQ4_NL, Q4_K or Q6_K blocks (K-contiguous rows), and QuantizedEmbeddingLookup.
+//
+// Reference semantics: quantizedDenseGGML (internal/gobackend/fusedops/quantizeddense_ggml.go:
+// 103-130): per output, the row dequantised to f32 (dequantXXXRow, :158-302), dotted with x in k
+// order, then the bias added, then the activation epilogue (fusedops/dense.go:176-205); x and
+// the output are f32 (:58-60).  execQuantizedEmbeddingLookup (fusedops/quantizeddense.go:455-499):
+// each index selects a row, dequantised to f32; an index outside [0, vocab) is an error.
+//
+// Kernels:
+//   ggml_dense_exact — one output column per thread, k in order, every value dequantised and
+//                      every product and sum rounded as the reference rounds them: bit-identical
+//                      to the reference's f32 result.
+//   ggml_gemv<T, MR> — M <= 4 rows (decode): a wave per output column at a time, the column's row
+//                      of blocks staged through LDS with 16-byte loads (a row is contiguous), x in
+//                      LDS as [m][32-value unit][36] (padded so that the 16 lanes of a 16-byte
+//                      read hit distinct banks).  Each lane takes 32-value units: their integer
+//                      codes times x are summed in f32 and the unit's scale (and min) applied
+//                      once, then the wave adds its lanes in a fixed tree.  f32 FMAs on the VALU:
+//                      x is f32 by contract, and bf16 matrix-core operands would not keep the
+//                      f32 accumulation bound.
+//   ggml_embed       — one thread per output value (the reference's arithmetic, bit-identical);
+//                      indices of any integer dtype, bad indices reported after the launch.
+#include <algorithm>
+#include <cstring>
+
+#include "device_common.h"
+#include "mxrt_internal.h"
+
+namespace mx {
+
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
+
+__host__ __device__ constexpr int ggml_vpb(int t) {
+  return (t == MX_GGML_Q4_0 || t == MX_GGML_Q8_0 || t == MX_GGML_IQ4_NL) ? 32
+         : (t == MX_GGML_Q4_K || t == MX_GGML_Q6_K)                        ? 256
+                                                                            : 0;
+}
+__host__ __device__ constexpr int ggml_bpb(int t) {
+  return (t == MX_GGML_Q4_0 || t == MX_GGML_IQ4_NL) ? 18
+         : t == MX_GGML_Q8_0                        ? 34
+         : t == MX_GGML_Q4_K                        ? 144
+         : t == MX_GGML_Q6_K                        ? 210
+                                                    : 0;
+}
+
+int ggml_block_geometry(int type, int* vpb, int* bpb) {
+  *vpb = ggml_vpb(type);
+  *bpb = ggml_bpb(type);
+  return *vpb ? MX_OK : set_error(MX_ERR_NOT_IMPLEMENTED, "GGML type %d not supported in fused path", type);
+}
+
+// Float16.Float32 (dtypes/float16/float16.go:17-60) on the bit pattern: exact, NaN payload kept.
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu;
+  uint32_t mant = h & 0x3FFu;
+  uint32_t bits;
+  if (e == 0x1Fu) {
+    bits = sign | 0x7F800000u | (mant << 13);
+  } else if (e == 0) {
+    if (mant == 0) {
+      bits = sign;
+    } else {
+      const int sh = __clz(mant) - 21;  // moves the leading one to bit 10
+      mant = (mant << sh) & 0x3FFu;
+      bits = sign | ((uint32_t)(1 - sh - 15 + 127) << 23) | (mant << 13);
+    }
+  } else {
+    bits = sign | ((e + 112u) << 23) | (mant << 13);
+  }
+  return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ float f16_at(const uint8_t* p) { return f16_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8)); }
+
+// compute.IQ4NLLookupTable (fused_ops.go:127-130).
+__constant__ static const float kIQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                              1,    13,   25,  38,  53,  69,  89,  113};
+
+// getScaleMinK4 (quantizeddense_ggml.go:229-239).
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* s, uint32_t* sc, uint32_t* m) {
+  if (j < 4) {
+    *sc = s[j] & 63u;
+    *m = s[j + 4] & 63u;
+  } else {
+    *sc = (s[j + 4] & 0xFu) | ((uint32_t)(s[j - 4] >> 6) << 4);
+    *m = (uint32_t)(s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
+  }
+}
+
+// Value i of a block, with the reference's f32 operations (dequantXXXRow).
+__device__ __forceinline__ float ggml_value(int t, const uint8_t* blk, int i) {
+  switch (t) {
+    case MX_GGML_Q8_0:
+      return mul_rn(f16_at(blk), (float)(int8_t)blk[2 + i]);
+    case MX_GGML_Q4_0: {
+      const uint32_t b = blk[2 + (i & 15)];
+      return mul_rn(f16_at(blk), (float)((int)(i < 16 ? b & 15u : b >> 4) - 8));
+    }
+    case MX_GGML_IQ4_NL: {
+      const uint32_t b = blk[2 + (i & 15)];
+      return mul_rn(f16_at(blk), kIQ4NL[i < 16 ? b & 15u : b >> 4]);
+    }
+    case MX_GGML_Q4_K: {
+      const int chunk = i >> 6, w = i & 63, j = 2 * chunk + (w >> 5), l = w & 31;
+      uint32_t sc, m;
+      scale_min_k4(j, blk + 4, &sc, &m);
+      const uint32_t b = blk[16 + 32 * chunk + l];
+      const float d1 = mul_rn(f16_at(blk), (float)sc), min1 = mul_rn(f16_at(blk + 2), (float)m);
+      return add_rn(mul_rn(d1, (float)(w < 32 ? b & 15u : b >> 4)), -min1);
+    }
+    default: {  // MX_GGML_Q6_K
+      const int h = i >> 7, r = i & 127, j = r >> 5, l = r & 31;
+      const uint32_t qlb = blk[64 * h + 32 * (j & 1) + l];
+      const uint32_t nib = (j >> 1) ? qlb >> 4 : qlb & 15u;
+      const uint32_t hi2 = (blk[128 + 32 * h + l] >> (2 * j)) & 3u;
+      const int q = (int)(nib | (hi2 << 4)) - 32;
+      const int sc = (int8_t)blk[192 + 8 * h + 2 * j + (l >> 4)];
+      return mul_rn(mul_rn(f16_at(blk + 208), (float)sc), (float)q);
+    }
+  }
+}
+
+// =============================================================================================
+// Reference-order dense kernel.
+// =============================================================================================
+constexpr int kGxThreads = 256;
+constexpr int kGxRows = 8;
+
+__global__ __launch_bounds__(kGxThreads) void ggml_dense_exact_kernel(GgmlDesc d) {
+  const int64_t n = (int64_t)blockIdx.x * kGxThreads + threadIdx.x;
+  const int64_t m0 = (int64_t)blockIdx.y * kGxRows;
+  if (n >= d.N) return;
+  const int rows = (int)min<int64_t>(kGxRows, d.M - m0);
+  const int vpb = ggml_vpb(d.type), bpb = ggml_bpb(d.type);
+  const uint8_t* row = d.w + n * d.bpr;
+  float acc[kGxRows];
+#pragma unroll
+  for (int r = 0; r < kGxRows; ++r) acc[r] = 0.0f;
+  for (int64_t k = 0; k < d.K; ++k) {
+    const float wv = ggml_value(d.type, row + (k / vpb) * bpb, (int)(k % vpb));
+#pragma unroll
+    for (int r = 0; r < kGxRows; ++r)
+      if (r < rows) acc[r] = add_rn(acc[r], mul_rn(d.x[(m0 + r) * d.K + k], wv));
+  }
+#pragma unroll
+  for (int r = 0; r < kGxRows; ++r)
+    if (r < rows) {
+      float v = acc[r];
+      if (d.bias) v = add_rn(v, d.bias[n]);
+      d.out[(m0 + r) * d.N + n] = act_ref(v, d.act);
+    }
+}
+
+// =============================================================================================
+// Decode GEMV.
+// =============================================================================================
+constexpr int kGvWaves = 8;
+constexpr int kGvThreads = 64 * kGvWaves;
+constexpr int kGvPad = 36;  // floats per 32-value unit of x in LDS
+
+// Sum over one 32-value unit u of the row (starting at `row` in LDS) of x[m][32u + l] * w, for
+// each of the MR rows of x (xu[m] points at the unit in LDS).
+template <int T, int MR>
+__device__ __forceinline__ void ggml_unit(const uint8_t* row, int u, const float* const (&xu)[MR], float (&acc)[MR]) {
+  // x of the unit, 8 x 16 bytes per row of x.
+  auto xv = [&](int m, int l) { return xu[m][l]; };
+  if constexpr (T == MX_GGML_Q4_0 || T == MX_GGML_IQ4_NL) {
+    const uint8_t* blk = row + 18 * u;
+    const float d = f16_at(blk);
+    float s[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) s[m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+      const uint32_t two = *(const uint16_t*)(blk + 2 + j);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t b = (two >> (8 * e)) & 0xFFu;
+        float lo, hi;
+        if constexpr (T == MX_GGML_Q4_0) {
+          lo = (float)((int)(b & 15u) - 8);
+          hi = (float)((int)(b >> 4) - 8);
+        } else {
+          lo = kIQ4NL[b & 15u];
+          hi = kIQ4NL[b >> 4];
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) s[m] = fmaf(xv(m, 16 + j + e), hi, fmaf(xv(m, j + e), lo, s[m]));
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = fmaf(d, s[m], acc[m]);
+  } else if constexpr (T == MX_GGML_Q8_0) {
+    const uint8_t* blk = row + 34 * u;
+    const float d = f16_at(blk);
+    float s[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) s[m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j += 2) {
+      const uint32_t two = *(const uint16_t*)(blk + 2 + j);
+      const float q0 = (float)(int8_t)(two & 0xFFu), q1 = (float)(int8_t)(two >> 8);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) s[m] = fmaf(xv(m, j + 1), q1, fmaf(xv(m, j), q0, s[m]));
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = fmaf(d, s[m], acc[m]);
+  } else if constexpr (T == MX_GGML_Q4_K) {
+    const int jj = u & 7;
+    const uint8_t* blk = row + 144 * (u >> 3);
+    uint32_t sc, mn;
+    scale_min_k4(jj, blk + 4, &sc, &mn);
+    const float a = f16_at(blk) * (float)sc, b = f16_at(blk + 2) * (float)mn;
+    const uint8_t* qs = blk + 16 + 32 * (jj >> 1);
+    const int sh = 4 * (jj & 1);
+    float s[MR], sx[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) s[m] = sx[m] = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 32; l += 2) {
+      const uint32_t two = *(const uint16_t*)(qs + l);
+      const float q0 = (float)((two >> sh) & 15u), q1 = (float)((two >> (8 + sh)) & 15u);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        s[m] = fmaf(xv(m, l + 1), q1, fmaf(xv(m, l), q0, s[m]));
+        sx[m] += xv(m, l) + xv(m, l + 1);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = fmaf(a, s[m], fmaf(-b, sx[m], acc[m]));
+  } else {  // MX_GGML_Q6_K: unit = quarter j of half h of a super-block
+    const int v = u & 7, h = v >> 2, j = v & 3;
+    const uint8_t* blk = row + 210 * (u >> 3);
+    const float d = f16_at(blk + 208);
+    const uint8_t* ql = blk + 64 * h + 32 * (j & 1);
+    const uint8_t* qh = blk + 128 + 32 * h;
+    const int nsh = 4 * (j >> 1), hsh = 2 * j;
+    const float sc0 = d * (float)(int8_t)blk[192 + 8 * h + 2 * j], sc1 = d * (float)(int8_t)blk[192 + 8 * h + 2 * j + 1];
+    float s0[MR], s1[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) s0[m] = s1[m] = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 32; l += 2) {
+      const uint32_t lo2 = *(const uint16_t*)(ql + l), hi2 = *(const uint16_t*)(qh + l);
+      const float q0 = (float)((int)(((lo2 >> nsh) & 15u) | (((hi2 >> hsh) & 3u) << 4)) - 32);
+      const float q1 = (float)((int)(((lo2 >> (8 + nsh)) & 15u) | (((hi2 >> (8 + hsh)) & 3u) << 4)) - 32);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if (l < 16)
+          s0[m] = fmaf(xv(m, l + 1), q1, fmaf(xv(m, l), q0, s0[m]));
+        else
+          s1[m] = fmaf(xv(m, l + 1), q1, fmaf(xv(m, l), q0, s1[m]));
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = fmaf(sc0, s0[m], fmaf(sc1, s1[m], acc[m]));
+  }
+}
+
+template <int T, int MR>
+__global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d, int row_stride) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int K = (int)d.K, units = K >> 5;
+  float* xs = (float*)lds;                                                  // [MR][units][kGvPad]
+  uint8_t* rows = lds + (size_t)MR * units * kGvPad * sizeof(float);        // [waves][row_stride]
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  for (int i = t; i < MR * K; i += kGvThreads) {
+    const int m = i / K, k = i - m * K;
+    xs[(m * units + (k >> 5)) * kGvPad + (k & 31)] = d.x[(size_t)m * K + k];
+  }
+  __syncthreads();
+
+  uint8_t* rb = rows + (size_t)wave * row_stride;
+  // The weights are read in whole 16-byte units from a 16-byte-aligned base: the buffer's range
+  // is its size rounded up to 16 (a partially valid unit must come back whole; the bytes past
+  // the end lie in the same allocation granule, 256 bytes or more) and units beyond it read 0.
+  const int64_t total = (d.N * d.bpr + 15) & ~(int64_t)15;
+  const __amdgpu_buffer_rsrc_t wrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(d.w), (short)0, (int)total, 0x00020000);
+  for (int64_t n = (int64_t)blockIdx.x * kGvWaves + wave; n < d.N; n += (int64_t)gridDim.x * kGvWaves) {
+    // Stage the row: 16-byte loads from the aligned address at or below its start, the row then
+    // begins `skew` bytes into the buffer.
+    const int64_t base = n * d.bpr, a0 = base & ~(int64_t)15;
+    const int skew = (int)(base - a0);
+    const int nch = (int)((base + d.bpr - a0 + 15) >> 4);
+    for (int c = lane; c < nch; c += 64)
+      *(u32x4_v*)(rb + 16 * c) = __builtin_amdgcn_raw_buffer_load_b128(wrs, (unsigned)(a0 + 16 * c), 0, 0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    const uint8_t* row = rb + skew;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+    for (int u = lane; u < units; u += 64) {
+      const float* xu[MR];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) xu[m] = xs + (size_t)(m * units + u) * kGvPad;
+      ggml_unit<T, MR>(row, u, xu, acc);
+    }
+    // Lanes in a fixed tree.
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        float v = acc[m];
+        if (d.bias) v = add_rn(v, d.bias[n]);
+        d.out[(size_t)m * d.N + n] = act_ref(v, d.act);
+      }
+    }
+    // Every lane's reads of the row are done before the next row is staged over it.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  }
+}
+
+// LDS of the GEMV for these sizes, or 0 if it does not apply.
+static size_t ggml_gemv_lds(const GgmlDesc& d, int* row_stride) {
+  if (d.M < 1 || d.M > 4 || d.K % 32 != 0 || d.K > (1 << 20) || d.N * d.bpr + 16 >= ((int64_t)1 << 31) ||
+      (uintptr_t)d.w % 16 != 0)
+    return 0;
+  const int64_t rs = ((d.bpr + 15 + 15) / 16) * 16;
+  const size_t bytes = (size_t)d.M * (d.K / 32) * kGvPad * sizeof(float) + (size_t)kGvWaves * rs;
+  if (bytes > 150 * 1024) return 0;
+  *row_stride = (int)rs;
+  return bytes;
+}
+
+bool ggml_gemv_fits(const GgmlDesc& d) {
+  int rs;
+  return ggml_gemv_lds(d, &rs) != 0;
+}
+
+template <int T>
+static void launch_gemv_t(const GgmlDesc& d, int grid, size_t lds, int rs, hipStream_t st) {
+  switch (d.M) {
+    case 1: dispatch(ggml_gemv_kernel<T, 1>, grid, kGvThreads, lds, st, d, rs); break;
+    case 2: dispatch(ggml_gemv_kernel<T, 2>, grid, kGvThreads, lds, st, d, rs); break;
+    case 3: dispatch(ggml_gemv_kernel<T, 3>, grid, kGvThreads, lds, st, d, rs); break;
+    default: dispatch(ggml_gemv_kernel<T, 4>, grid, kGvThreads, lds, st, d, rs); break;
+  }
+}
+
+const char* ggml_plan_name(const GgmlDesc& d) {
+  if (d.M == 0 || d.N == 0) return "empty";
+  return ggml_gemv_fits(d) ? "ggml_gemv" : "ggml_dense_exact";
+}
+
+int ggml_dense_run(mx_backend* b, const GgmlDesc& d) {
+  MX_TRY(check_device(b));
+  if (d.M == 0 || d.N == 0) return MX_OK;
+  hipStream_t st = b->stream;
+  int rs = 0;
+  const size_t lds = ggml_gemv_lds(d, &rs);
+  if (lds) {
+    const int grid = (int)std::min<int64_t>((d.N + kGvWaves - 1) / kGvWaves, 2 * (int64_t)std::max(b->num_cus, 1));
+    return launch(b, "ggml_gemv", [&] {
+      switch (d.type) {
+        case MX_GGML_Q4_0: launch_gemv_t<MX_GGML_Q4_0>(d, grid, lds, rs, st); break;
+        case MX_GGML_Q8_0: launch_gemv_t<MX_GGML_Q8_0>(d, grid, lds, rs, st); break;
+        case MX_GGML_IQ4_NL: launch_gemv_t<MX_GGML_IQ4_NL>(d, grid, lds, rs, st); break;
+        case MX_GGML_Q4_K: launch_gemv_t<MX_GGML_Q4_K>(d, grid, lds, rs, st); break;
+        default: launch_gemv_t<MX_GGML_Q6_K>(d, grid, lds, rs, st); break;
+      }
+    });
+  }
+  dim3 grid((unsigned)((d.N + kGxThreads - 1) / kGxThreads), (unsigned)((d.M + kGxRows - 1) / kGxRows));
+  if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "FusedQuantizedDense(GGML): M too large");
+  return launch(b, "ggml_dense_exact", [&] { dispatch(ggml_dense_exact_kernel, grid, kGxThreads, 0, st, d); });
+}
+
+// =============================================================================================
+// QuantizedEmbeddingLookup.
+// =============================================================================================
+__device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int dt) {
+  switch (dt) {
+    case MX_DTYPE_INT8: return ((const int8_t*)p)[i];
+    case MX_DTYPE_INT16: return ((const int16_t*)p)[i];
+    case MX_DTYPE_INT32: return ((const int32_t*)p)[i];
+    case MX_DTYPE_UINT8: return ((const uint8_t*)p)[i];
+    case MX_DTYPE_UINT16: return ((const uint16_t*)p)[i];
+    case MX_DTYPE_UINT32: return ((const uint32_t*)p)[i];
+    case MX_DTYPE_UINT64: {
+      const uint64_t v = ((const uint64_t*)p)[i];
+      return v > (uint64_t)INT64_MAX ? -1 : (int64_t)v;
+    }
+    default: return ((const int64_t*)p)[i];
+  }
+}
+
+// One thread per output value; a bad index writes nothing and records its position (the
+// smallest one) in *bad, which the host reads back.
+__global__ void ggml_embed_kernel(GgmlEmbedDesc e, unsigned long long* bad) {
+  const int64_t total = e.n * e.K;
+  const int vpb = ggml_vpb(e.type), bpb = ggml_bpb(e.type);
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < total; p += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = p / e.K, k = p - i * e.K;
+    const int64_t r = load_index(e.idx, i, e.idx_dt);
+    if (r < 0 || r >= e.vocab) {
+      if (k == 0) atomicMin(bad, (unsigned long long)i);
+      continue;
+    }
+    e.out[p] = ggml_value(e.type, e.data + r * e.bpr + (k / vpb) * bpb, (int)(k % vpb));
+  }
+}
+
+__global__ void ggml_fill_u64(unsigned long long* p, unsigned long long v) { *p = v; }
+
+int ggml_embed_run(mx_backend* b, const GgmlEmbedDesc& e) {
+  MX_TRY(check_device(b));
+  if (e.n == 0 || e.K == 0) return MX_OK;
+  void* flag = nullptr;
+  MX_TRY(dev_alloc(b, sizeof(unsigned long long), &flag));
+  unsigned long long* bad = (unsigned long long*)flag;
+  hipStream_t st = b->stream;
+  const int64_t total = e.n * e.K;
+  const int grid = (int)std::min<int64_t>((total + 255) / 256, 65536);
+  int rc = launch(b, "ggml_embed", [&] {
+    dispatch(ggml_fill_u64, 1, 1, 0, st, bad, ~0ull);
+    dispatch(ggml_embed_kernel, grid, 256, 0, st, e, bad);
+  });
+  unsigned long long h = ~0ull;
+  if (rc == MX_OK) {
+    // The reference reports an out-of-range index as an error of the call, so the result of
+    // the check has to be known before returning.
+    if (hipMemcpyAsync(&h, bad, sizeof(h), hipMemcpyDeviceToHost, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+      rc = set_error(MX_ERR_HIP, "QuantizedEmbeddingLookup: reading the index check failed");
+  }
+  dev_free(b, flag);
+  if (rc != MX_OK || h == ~0ull) return rc;
+  // The offending value, for the message the reference gives.
+  const int isz = (e.idx_dt == MX_DTYPE_INT8 || e.idx_dt == MX_DTYPE_UINT8)     ? 1
+                  : (e.idx_dt == MX_DTYPE_INT16 || e.idx_dt == MX_DTYPE_UINT16) ? 2
+                  : (e.idx_dt == MX_DTYPE_INT32 || e.idx_dt == MX_DTYPE_UINT32) ? 4
+                                                                                : 8;
+  uint8_t raw[8] = {0};
+  if (hipMemcpy(raw, (const uint8_t*)e.idx + h * isz, isz, hipMemcpyDeviceToHost) != hipSuccess)
+    return set_error(MX_ERR_HIP, "QuantizedEmbeddingLookup: reading the bad index failed");
+  long long v = 0;
+  switch (e.idx_dt) {
+    case MX_DTYPE_INT8: v = *(int8_t*)raw; break;
+    case MX_DTYPE_INT16: v = *(int16_t*)raw; break;
+    case MX_DTYPE_INT32: v = *(int32_t*)raw; break;
+    case MX_DTYPE_UINT8: v = *(uint8_t*)raw; break;
+    case MX_DTYPE_UINT16: v = *(uint16_t*)raw; break;
+    case MX_DTYPE_UINT32: v = *(uint32_t*)raw; break;
+    default: memcpy(&v, raw, 8); break;
+  }
+  return set_error(MX_ERR_INVALID, "QuantizedEmbeddingLookup: index %lld out of range [0, %lld)", v, (long long)e.vocab);
+}
+
+}  // namespace mx
+
+// =============================================================================================
+// C ABI: direct embedding lookup.
+// =============================================================================================
+extern "C" int mx_quantized_embedding_lookup(mx_backend* b, const mx_qembed_args* a) {
+  mx::clear_error();
+  MX_TRY(mx::check_device(b));
+  const char* op = "QuantizedEmbeddingLookup";
+  if (!a) return mx::set_error(MX_ERR_INVALID, "%s: args is NULL", op);
+  int vpb, bpb;
+  switch (a->ggml_type) {
+    case MX_GGML_Q4_0: case MX_GGML_Q8_0: case MX_GGML_IQ4_NL: case MX_GGML_Q4_K: case MX_GGML_Q6_K: break;
+    default:
+      return mx::set_error(MX_ERR_NOT_IMPLEMENTED, "%s: GGML type %d not supported in fused path", op, a->ggml_type);
+  }
+  MX_TRY(mx::ggml_block_geometry(a->ggml_type, &vpb, &bpb));
+  switch (a->index_dtype) {
+    case MX_DTYPE_INT8: case MX_DTYPE_INT16: case MX_DTYPE_INT32: case MX_DTYPE_INT64:
+    case MX_DTYPE_UINT8: case MX_DTYPE_UINT16: case MX_DTYPE_UINT32: case MX_DTYPE_UINT64: break;
+    default: return mx::set_error(MX_ERR_INVALID, "%s: indices must be integer, got %s", op, mx::dtype_name(a->index_dtype));
+  }
+  if (a->bytes_per_row < 0 || a->bytes_per_row % bpb != 0 || a->vocab < 0 || a->n < 0)
+    return mx::set_error(MX_ERR_INVALID, "%s: bytesPerRow %lld not divisible by bytesPerBlock %d", op,
+                         (long long)a->bytes_per_row, bpb);
+  mx::GgmlEmbedDesc e;
+  e.data = (const uint8_t*)a->data;
+  e.idx = a->indices;
+  e.out = (float*)a->out;
+  e.vocab = a->vocab;
+  e.bpr = a->bytes_per_row;
+  e.K = a->bytes_per_row / bpb * vpb;
+  e.n = a->n;
+  e.idx_dt = a->index_dtype;
+  e.type = a->ggml_type;
+  if (e.n * e.K > 0 && (!e.out || !e.idx || !e.data)) return mx::set_error(MX_ERR_INVALID, "%s: NULL data pointer", op);
+  std::lock_guard<std::recursive_mutex> lk(b->mu);
+  return mx::ggml_embed_run(b, e);
+}

@@ -40,7 +40,8 @@ enum class Op {
   kBiasAct,
   kGelu,
   kCopy,
-  kRmsNorm,  // fused row RMS normalisation (compile-time fusion)
+  kRmsNorm,
+  kQEmbed,  // fused row RMS normalisation (compile-time fusion)
 };
 
 static const char* op_name(Op op) {
@@ -61,6 +62,7 @@ static const char* op_name(Op op) {
     case Op::kGelu: return "FusedGelu";
     case Op::kCopy: return "Copy";
     case Op::kRmsNorm: return "RmsNorm";
+    case Op::kQEmbed: return "QuantizedEmbeddingLookup";
   }
   return "?";
 }
@@ -77,6 +79,8 @@ struct Node {
   std::vector<uint8_t> data;
   // FusedQuantizedDense.
   int scheme = 0, block_axis = 0, block_size = 0, act = 0;
+  int ggml_type = 0;
+  int64_t bpr = 0;  // GGML: bytes per weight row
   bool has_zp = false, has_bias = false;
   int res_op = 0;  // elementwise op folded into the epilogue (operand = last input)
   int64_t M = 0, K = 0, N = 0;
@@ -260,7 +264,7 @@ static bool supported_op(int op) {
     case MX_OP_MAX: case MX_OP_MIN: case MX_OP_MUL: case MX_OP_NEG: case MX_OP_REDUCE_MAX:
     case MX_OP_REDUCE_SUM: case MX_OP_RESHAPE: case MX_OP_RSQRT: case MX_OP_SLICE: case MX_OP_SQRT:
     case MX_OP_SUB: case MX_OP_TANH: case MX_OP_TRANSPOSE: case MX_OP_FUSED_GELU: case MX_OP_FUSED_DENSE:
-    case MX_OP_FUSED_QUANTIZED_DENSE:
+    case MX_OP_FUSED_QUANTIZED_DENSE: case MX_OP_QUANTIZED_EMBEDDING_LOOKUP:
       return true;
     default:
       return false;
@@ -395,6 +399,113 @@ int mx_fn_return(mx_function* fn, const mx_value* outputs, int n) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// GGML block formats (reference builders: internal/gobackend/fusedops/quantizeddense.go:144-321).
+// ---------------------------------------------------------------------------------------------
+// validateGGMLTypeSupported + deriveGGMLK (quantizeddense.go:145-177).
+static int ggml_derive_k(const char* op, int type, int64_t bytes_per_row, int64_t* K) {
+  switch (type) {
+    case MX_GGML_Q4_0: case MX_GGML_Q8_0: case MX_GGML_IQ4_NL: case MX_GGML_Q4_K: case MX_GGML_Q6_K: break;
+    default: return set_error(MX_ERR_NOT_IMPLEMENTED, "%s: GGML type %d not supported in fused path", op, type);
+  }
+  int vpb, bpb;
+  MX_TRY(ggml_block_geometry(type, &vpb, &bpb));
+  if (bytes_per_row % bpb != 0)
+    return set_error(MX_ERR_INVALID, "%s: bytesPerRow %lld not divisible by bytesPerBlock %d", op,
+                     (long long)bytes_per_row, bpb);
+  *K = bytes_per_row / bpb * vpb;
+  return MX_OK;
+}
+
+// FusedQuantizedDenseGGML (quantizeddense.go:181-248): x [batch..., K] f32, w [N, bytesPerRow]
+// Uint8, bias [N] f32; output [batch..., N] f32.
+static int fused_quantized_dense_ggml(mx_function* fn, mx_value xv, mx_value wv, mx_value biasv,
+                                      const mx_quantization* q, int activation, mx_value* out) {
+  const char* op = "FusedQuantizedDense(GGML)";
+  int x, w, bias = -1;
+  MX_TRY(get_node(fn->bld, xv, op, &x));
+  MX_TRY(get_node(fn->bld, wv, op, &w));
+  if (biasv) MX_TRY(get_node(fn->bld, biasv, op, &bias));
+  const Shape xs = shape_of(fn, x), ws = shape_of(fn, w);
+  if (xs.dtype != MX_DTYPE_FLOAT32)
+    return set_error(MX_ERR_INVALID, "%s: x must be float32, got %s", op, dtype_name(xs.dtype));
+  if (xs.rank() < 1) return set_error(MX_ERR_INVALID, "%s: x must have rank >= 1, got %d", op, xs.rank());
+  if (ws.rank() != 2 || ws.dtype != MX_DTYPE_UINT8)
+    return set_error(MX_ERR_INVALID, "%s: weights must be [N, bytesPerRow] Uint8, got %s", op, ws.str().c_str());
+  const int64_t N = ws.dims[0], bpr = ws.dims[1];
+  int64_t K = 0;
+  MX_TRY(ggml_derive_k(op, q->ggml_type, bpr, &K));
+  if (xs.dims.back() != K)
+    return set_error(MX_ERR_INVALID, "%s: x's last dim (%lld) must match K=%lld derived from weights", op,
+                     (long long)xs.dims.back(), (long long)K);
+  if (q->zero_point) return set_error(MX_ERR_INVALID, "%s: ZeroPoint must be nil for GGML scheme", op);
+  if (bias >= 0) {
+    const Shape bs = shape_of(fn, bias);
+    if (bs.rank() != 1 || bs.dims[0] != N || bs.dtype != MX_DTYPE_FLOAT32)
+      return set_error(MX_ERR_INVALID, "%s: bias must be [%lld] float32, got %s", op, (long long)N, bs.str().c_str());
+  }
+  if (activation < MX_ACT_NONE || activation > MX_ACT_TANH)
+    return set_error(MX_ERR_INVALID, "%s: unknown activation %d", op, activation);
+  Node n;
+  n.op = Op::kQDense;
+  n.shape.dtype = MX_DTYPE_FLOAT32;
+  n.shape.dims = xs.dims;
+  n.shape.dims.back() = N;
+  n.in = {x, w};
+  if (bias >= 0) n.in.push_back(bias);
+  n.scheme = MX_QUANT_GGML;
+  n.ggml_type = q->ggml_type;
+  n.bpr = bpr;
+  n.act = activation;
+  n.has_bias = bias >= 0;
+  n.K = K;
+  n.N = N;
+  n.M = 1;
+  for (int i = 0; i + 1 < xs.rank(); ++i) n.M *= xs.dims[i];
+  return add_node(fn, std::move(n), out);
+}
+
+// QuantizedEmbeddingLookup (quantizeddense.go:266-321).
+int mx_fn_quantized_embedding_lookup(mx_function* fn, mx_value datav, mx_value idxv, const mx_quantization* q,
+                                     mx_value* out) {
+  clear_error();
+  const char* op = "QuantizedEmbeddingLookup";
+  MX_TRY(check_fn(fn, op));
+  if (!q) return set_error(MX_ERR_INVALID, "%s: quantization is nil", op);
+  if (q->scheme != MX_QUANT_GGML)
+    return set_error(MX_ERR_NOT_IMPLEMENTED,
+                     "%s: only QuantGGML scheme is supported, got %d -- please create a feature request if you need "
+                     "support for a different quantization scheme",
+                     op, q->scheme);
+  int data, idx;
+  MX_TRY(get_node(fn->bld, datav, op, &data));
+  MX_TRY(get_node(fn->bld, idxv, op, &idx));
+  const Shape ds = shape_of(fn, data), is = shape_of(fn, idx);
+  if (ds.rank() != 2 || ds.dtype != MX_DTYPE_UINT8)
+    return set_error(MX_ERR_INVALID, "%s: data must be [vocabSize, bytesPerRow] Uint8, got %s", op, ds.str().c_str());
+  switch (is.dtype) {
+    case MX_DTYPE_INT8: case MX_DTYPE_INT16: case MX_DTYPE_INT32: case MX_DTYPE_INT64:
+    case MX_DTYPE_UINT8: case MX_DTYPE_UINT16: case MX_DTYPE_UINT32: case MX_DTYPE_UINT64: break;
+    default: return set_error(MX_ERR_INVALID, "%s: indices must be integer, got %s", op, dtype_name(is.dtype));
+  }
+  if (is.rank() < 1 || is.dims.back() != 1)
+    return set_error(MX_ERR_INVALID, "%s: indices last dim must be 1, got shape %s", op, is.str().c_str());
+  int64_t K = 0;
+  MX_TRY(ggml_derive_k(op, q->ggml_type, ds.dims[1], &K));
+  Node n;
+  n.op = Op::kQEmbed;
+  n.shape.dtype = MX_DTYPE_FLOAT32;
+  n.shape.dims = is.dims;
+  n.shape.dims.back() = K;
+  n.in = {data, idx};
+  n.ggml_type = q->ggml_type;
+  n.bpr = ds.dims[1];
+  n.K = K;
+  n.N = ds.dims[0];  // vocabulary size
+  n.M = is.size();   // number of indices
+  return add_node(fn, std::move(n), out);
+}
+
+// ---------------------------------------------------------------------------------------------
 // FusedQuantizedDense (reference builder: internal/gobackend/fusedops/quantizeddense.go:58-142).
 // ---------------------------------------------------------------------------------------------
 int mx_fn_fused_quantized_dense(mx_function* fn, mx_value xv, mx_value wv, mx_value biasv,
@@ -403,8 +514,7 @@ int mx_fn_fused_quantized_dense(mx_function* fn, mx_value xv, mx_value wv, mx_va
   const char* op = "FusedQuantizedDense";
   MX_TRY(check_fn(fn, op));
   if (!q) return set_error(MX_ERR_INVALID, "%s: quantization is nil", op);
-  if (q->scheme == MX_QUANT_GGML)
-    return set_error(MX_ERR_NOT_IMPLEMENTED, "%s: GGML block formats are not implemented", op);
+  if (q->scheme == MX_QUANT_GGML) return fused_quantized_dense_ggml(fn, xv, wv, biasv, q, activation, out);
   if (q->scheme != MX_QUANT_LINEAR && q->scheme != MX_QUANT_NF4)
     return set_error(MX_ERR_NOT_IMPLEMENTED, "%s: unknown quantization scheme %d", op, q->scheme);
   int x, w, s, zp = -1, bias = -1;
@@ -994,7 +1104,7 @@ static void fuse_dense_epilogues(const FunctionImpl& f, std::vector<Node>& nodes
     for (int side = 1; side >= 0; --side) {
       const int c = n.in[side];
       const Node& cn = nodes[c];
-      if (cn.op == Op::kQDense && cn.res_op == 0 && uses[c] == 1 && cn.shape == n.shape) {
+      if (cn.op == Op::kQDense && cn.scheme != MX_QUANT_GGML && cn.res_op == 0 && uses[c] == 1 && cn.shape == n.shape) {
         q = c;
         r = n.in[1 - side];
         break;
@@ -1232,8 +1342,38 @@ static int run_node(mx_executable* e, int i, std::vector<void*>& ptr) {
   void* out = ptr[i];
   const int64_t count = n.shape.size();
   switch (n.op) {
+    case Op::kQEmbed: {
+      GgmlEmbedDesc g;
+      g.data = (const uint8_t*)in(0);
+      g.idx = in(1);
+      g.out = (float*)out;
+      g.vocab = n.N;
+      g.bpr = n.bpr;
+      g.K = n.K;
+      g.n = n.M;
+      g.idx_dt = ins(1).dtype;
+      g.type = n.ggml_type;
+      return ggml_embed_run(b, g);
+    }
     case Op::kQDense: {
       QDenseDesc d{};
+      if (n.scheme == MX_QUANT_GGML) {
+        d.x = in(0);
+        d.w = in(1);
+        d.bias = n.has_bias ? in(2) : nullptr;
+        d.out = out;
+        d.M = n.M;
+        d.K = n.K;
+        d.N = n.N;
+        d.x_dt = MX_DTYPE_FLOAT32;
+        d.w_dt = MX_DTYPE_UINT8;
+        d.b_dt = n.has_bias ? MX_DTYPE_FLOAT32 : 0;
+        d.scheme = MX_QUANT_GGML;
+        d.ggml_type = n.ggml_type;
+        d.bpr = n.bpr;
+        d.act = n.act;
+        return qdense_run(b, d);
+      }
       d.x = in(0);
       d.w = in(1);
       d.scale = in(2);

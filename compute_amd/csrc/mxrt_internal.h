@@ -211,6 +211,9 @@ struct QDenseDesc {
   // MX_OP_MUL), rounded again as the separate elementwise op would.
   const void* res = nullptr;
   int res_dt = 0, res_op = 0;
+  // GGML scheme: block format (MX_GGML_*) and bytes per weight row ([N, bpr] storage).
+  int ggml_type = 0;
+  int64_t bpr = 0;
 };
 int qdense_validate(const mx_qdense_args* a, QDenseDesc* d);
 int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name);
@@ -218,6 +221,29 @@ int qdense_run(mx_backend* b, const QDenseDesc& d);
 // Skinny-M MFMA kernel (qdense_skinny.hip): shape/layout check and launch.
 bool qdense_skinny_fits(const QDenseDesc& d);
 int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name);
+// GGML block formats (ggml.hip): FusedQuantizedDense with weights [N, bpr] bytes and f32 x/out,
+// and QuantizedEmbeddingLookup.
+struct GgmlDesc {
+  const float* x;      // [M, K]
+  const uint8_t* w;    // [N, bpr]
+  const float* bias;   // [N] or null
+  float* out;          // [M, N]
+  int64_t M = 0, K = 0, N = 0, bpr = 0;
+  int type = 0, act = 0;
+};
+struct GgmlEmbedDesc {
+  const uint8_t* data;  // [vocab, bpr]
+  const void* idx;      // n indices, idx_dt
+  float* out;           // [n, K]
+  int64_t vocab = 0, bpr = 0, K = 0, n = 0;
+  int idx_dt = 0, type = 0;
+};
+int ggml_block_geometry(int type, int* vpb, int* bpb);
+bool ggml_gemv_fits(const GgmlDesc& d);
+const char* ggml_plan_name(const GgmlDesc& d);
+int ggml_dense_run(mx_backend* b, const GgmlDesc& d);
+int ggml_embed_run(mx_backend* b, const GgmlEmbedDesc& e);
+
 // Prefill MFMA GEMM (qdense_gemm.hip): shape/layout check and launch.
 bool qdense_gemm_fits(const QDenseDesc& d);
 int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name);

@@ -32,10 +32,41 @@ namespace mx {
 // =============================================================================================
 static bool is_f32_or_bf16(int dt) { return dt == MX_DTYPE_FLOAT32 || dt == MX_DTYPE_BFLOAT16; }
 
+// FusedQuantizedDenseGGML's checks (quantizeddense.go:181-248) on the direct entry point's args.
+static int ggml_validate(const mx_qdense_args* a, QDenseDesc* d) {
+  const char* op = "FusedQuantizedDense(GGML)";
+  int vpb, bpb;
+  switch (a->ggml_type) {
+    case MX_GGML_Q4_0: case MX_GGML_Q8_0: case MX_GGML_IQ4_NL: case MX_GGML_Q4_K: case MX_GGML_Q6_K: break;
+    default: return set_error(MX_ERR_NOT_IMPLEMENTED, "%s: GGML type %d not supported in fused path", op, a->ggml_type);
+  }
+  MX_TRY(ggml_block_geometry(a->ggml_type, &vpb, &bpb));
+  if (a->x_dtype != MX_DTYPE_FLOAT32)
+    return set_error(MX_ERR_INVALID, "%s: x must be float32, got %s", op, dtype_name(a->x_dtype));
+  if (a->zero_point) return set_error(MX_ERR_INVALID, "%s: ZeroPoint must be nil for GGML scheme", op);
+  if (a->bias && a->bias_dtype != MX_DTYPE_FLOAT32)
+    return set_error(MX_ERR_INVALID, "%s: bias must be float32, got %s", op, dtype_name(a->bias_dtype));
+  if (a->activation < MX_ACT_NONE || a->activation > MX_ACT_TANH)
+    return set_error(MX_ERR_INVALID, "%s: unknown activation %d", op, a->activation);
+  if (a->M < 0 || a->K < 0 || a->N < 0 || a->K % vpb != 0)
+    return set_error(MX_ERR_INVALID, "%s: K=%lld must be a non-negative multiple of %d (M=%lld, N=%lld)", op,
+                     (long long)a->K, vpb, (long long)a->M, (long long)a->N);
+  if (a->K > (int64_t)1 << 31 || a->N > (int64_t)1 << 31) return set_error(MX_ERR_INVALID, "%s: K and N must be < 2^31", op);
+  if (a->M * a->N > 0 && (!a->out || (a->K > 0 && (!a->x || !a->w))))
+    return set_error(MX_ERR_INVALID, "%s: NULL data pointer", op);
+  *d = QDenseDesc{};
+  d->x = a->x; d->w = a->w; d->bias = a->bias; d->out = a->out;
+  d->M = a->M; d->K = a->K; d->N = a->N;
+  d->x_dt = MX_DTYPE_FLOAT32; d->w_dt = MX_DTYPE_UINT8; d->b_dt = a->bias ? MX_DTYPE_FLOAT32 : 0;
+  d->scheme = MX_QUANT_GGML; d->act = a->activation;
+  d->ggml_type = a->ggml_type;
+  d->bpr = a->K / vpb * bpb;
+  return MX_OK;
+}
+
 int qdense_validate(const mx_qdense_args* a, QDenseDesc* d) {
   if (!a) return set_error(MX_ERR_INVALID, "FusedQuantizedDense: args is NULL");
-  if (a->scheme == MX_QUANT_GGML)
-    return set_error(MX_ERR_NOT_IMPLEMENTED, "FusedQuantizedDense: GGML block formats are not implemented");
+  if (a->scheme == MX_QUANT_GGML) return ggml_validate(a, d);
   if (a->scheme != MX_QUANT_LINEAR && a->scheme != MX_QUANT_NF4)
     return set_error(MX_ERR_NOT_IMPLEMENTED, "FusedQuantizedDense: unknown quantization scheme %d", a->scheme);
   if (!is_f32_or_bf16(a->x_dtype))
@@ -124,8 +155,24 @@ __global__ __launch_bounds__(kExactThreads) void qdense_exact_kernel(QDenseDesc 
 // =============================================================================================
 enum class QPath { kEmpty, kExact, kSkinny, kGemm };
 
+static GgmlDesc ggml_desc(const QDenseDesc& d) {
+  GgmlDesc g;
+  g.x = (const float*)d.x;
+  g.w = (const uint8_t*)d.w;
+  g.bias = (const float*)d.bias;
+  g.out = (float*)d.out;
+  g.M = d.M;
+  g.K = d.K;
+  g.N = d.N;
+  g.bpr = d.bpr;
+  g.type = d.ggml_type;
+  g.act = d.act;
+  return g;
+}
+
 static QPath choose_path(const QDenseDesc& d) {
   if (d.M == 0 || d.N == 0) return QPath::kEmpty;
+  if (d.scheme == MX_QUANT_GGML) return QPath::kExact;
   if (qdense_skinny_fits(d)) return QPath::kSkinny;
   if (qdense_gemm_fits(d)) return QPath::kGemm;
   return QPath::kExact;
@@ -149,6 +196,10 @@ static const char* path_name(const QDenseDesc& d, QPath p) {
 
 int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name) {
   (void)b;
+  if (d.scheme == MX_QUANT_GGML) {
+    *name = ggml_plan_name(ggml_desc(d));
+    return MX_OK;
+  }
   *name = path_name(d, choose_path(d));
   return MX_OK;
 }
@@ -172,6 +223,7 @@ int qdense_run(mx_backend* b, const QDenseDesc& d) {
     dev_free(b, tmp);  // stream-ordered pool: later users run after these kernels
     return rc;
   }
+  if (d.scheme == MX_QUANT_GGML) return ggml_dense_run(b, ggml_desc(d));
   const char* name = path_name(d, p);
   hipStream_t st = b->stream;
   switch (p) {

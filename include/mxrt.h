@@ -66,6 +66,18 @@ enum {
 
 /* compute.QuantizationScheme (fused_ops.go:81-98). */
 enum { MX_QUANT_LINEAR = 0, MX_QUANT_NF4 = 1, MX_QUANT_GGML = 2 };
+/* compute.GGMLQuantType (fused_ops.go:134-146).  The fused paths support Q4_0, Q8_0, IQ4_NL, Q4_K
+ * and Q6_K, like the reference (quantizeddense.go:145-152). */
+enum {
+  MX_GGML_Q4_0 = 0,
+  MX_GGML_Q8_0 = 1,
+  MX_GGML_IQ4_NL = 2,
+  MX_GGML_Q2_K = 3,
+  MX_GGML_Q3_K = 4,
+  MX_GGML_Q4_K = 5,
+  MX_GGML_Q5_K = 6,
+  MX_GGML_Q6_K = 7
+};
 
 /* compute.ActivationType (fused_ops.go:280-289). */
 enum {
@@ -108,7 +120,8 @@ enum {
   MX_OP_TRANSPOSE = 104,
   MX_OP_FUSED_GELU = 118,
   MX_OP_FUSED_DENSE = 119,
-  MX_OP_FUSED_QUANTIZED_DENSE = 123
+  MX_OP_FUSED_QUANTIZED_DENSE = 123,
+  MX_OP_QUANTIZED_EMBEDDING_LOOKUP = 124
 };
 
 #define MX_MAX_RANK 8
@@ -236,15 +249,27 @@ typedef struct mx_quantization {
   mx_value zero_point; /* 0 = symmetric */
   int32_t block_axis;
   int32_t block_size;
-  int32_t ggml_type;   /* unused unless scheme == MX_QUANT_GGML (not implemented) */
+  int32_t ggml_type;   /* MX_GGML_*, used only when scheme == MX_QUANT_GGML (scale, zero_point,
+                          block_axis and block_size are then unused: the blocks embed them)   */
 } mx_quantization;
 
 /* FusedOps.FusedQuantizedDense (fused_ops.go:433-435; reference builder
  * internal/gobackend/fusedops/quantizeddense.go:58-142).  y = act(x @ dequant(w) + bias).
  * x: [batch..., K] float32 or bfloat16; w: [K, N] Int4/Uint4/Int8/Uint8; scale/zero_point/bias:
- * float32 or bfloat16; output dtype = x dtype.  bias may be 0. */
+ * float32 or bfloat16; output dtype = x dtype.  bias may be 0.
+ * GGML scheme (FusedQuantizedDenseGGML, quantizeddense.go:181-248): x [batch..., K] float32,
+ * w [N, bytesPerRow] Uint8 in q->ggml_type blocks (K = bytesPerRow / bytesPerBlock *
+ * valuesPerBlock), bias [N] float32 or 0, output float32; q->zero_point must be 0. */
 int mx_fn_fused_quantized_dense(mx_function* fn, mx_value x, mx_value w, mx_value bias,
                                 const mx_quantization* q, int activation, mx_value* out);
+
+/* FusedOps.QuantizedEmbeddingLookup (fused_ops.go:408-409; reference builder
+ * internal/gobackend/fusedops/quantizeddense.go:266-321).  data: [vocab, bytesPerRow] Uint8 in
+ * q->ggml_type blocks (q->scheme must be MX_QUANT_GGML, else MX_ERR_NOT_IMPLEMENTED); indices:
+ * any integer dtype, last dimension 1; output [indices dims[:-1]..., K] float32.  An index outside
+ * [0, vocab) makes Execute fail (execQuantizedEmbeddingLookup, quantizeddense.go:455-499). */
+int mx_fn_quantized_embedding_lookup(mx_function* fn, mx_value data, mx_value indices, const mx_quantization* q,
+                                     mx_value* out);
 
 /* StandardOps.DotGeneral (standard_ops.go:356-361), DotGeneralConfig (standard_ops.go:91-111).
  * accumulator_dtype / output_dtype may be MX_DTYPE_INVALID (= defaults). */
@@ -332,12 +357,26 @@ typedef struct mx_qdense_args {
   int32_t block_axis;     /* 0: blocks along K, scale [ceil(K/B), N]; 1: reference [K, ceil(N/B)] */
   int32_t block_size;
   int32_t activation;     /* MX_ACT_*                                                          */
+  int32_t ggml_type;      /* scheme MX_QUANT_GGML: MX_GGML_*; w is then [N, bytesPerRow] bytes,
+                             x, bias and out float32, K the logical input features             */
 } mx_qdense_args;
 
 /* Launches y = act(x @ dequant(w) + bias) on the backend's stream (asynchronous). */
 int mx_qdense(mx_backend* b, const mx_qdense_args* args);
 /* Name of the kernel family mx_qdense would pick for these arguments ("gemv_i4_dot2", ...). */
 int mx_qdense_plan(mx_backend* b, const mx_qdense_args* args, char* buf, size_t buflen);
+
+/* QuantizedEmbeddingLookup on device pointers (the Executable launches the same kernel);
+ * replaces execQuantizedEmbeddingLookup (internal/gobackend/fusedops/quantizeddense.go:455-499).
+ * Waits for the launch: an index outside [0, vocab) is reported as MX_ERR_INVALID. */
+typedef struct mx_qembed_args {
+  const void* data;       /* [vocab, bytes_per_row] GGML blocks                                */
+  const void* indices;    /* n indices of index_dtype (any integer dtype)                      */
+  void* out;              /* [n, K] float32                                                    */
+  int64_t vocab, bytes_per_row, n;
+  int32_t index_dtype, ggml_type;
+} mx_qembed_args;
+int mx_quantized_embedding_lookup(mx_backend* b, const mx_qembed_args* args);
 
 #ifdef __cplusplus
 }

@@ -379,3 +379,16 @@ def ggml_embedding(data, t: int, idx) -> np.ndarray:
     if rc != 0:
         raise IndexError(f"index {int(i[rc - 1])} out of range [0, {d.shape[0]})")
     return out
+
+
+def ggml_random_rows(t: int, n: int, k: int, rng) -> np.ndarray:
+    """Random GGML rows [n, bytesPerRow] with finite block scales in U(0.001, 0.02) (test data)."""
+    vpb, bpb = ggml_block(t)
+    nb = k // vpb
+    rows = rng.integers(0, 256, (n, nb, bpb), dtype=np.uint8)
+    scale_at = {GGML_Q4_0: [0], GGML_Q8_0: [0], GGML_IQ4_NL: [0], GGML_Q4_K: [0, 2], GGML_Q6_K: [208]}[t]
+    for off in scale_at:
+        d = rng.uniform(0.001, 0.02, (n, nb)).astype(np.float16).view(np.uint16)
+        rows[:, :, off] = d & 0xFF
+        rows[:, :, off + 1] = d >> 8
+    return rows.reshape(n, nb * bpb)

@@ -115,11 +115,69 @@ def test_qdense_validation_errors(host_backend, case):
         assert not ca.IsNotImplemented(ei.value)
 
 
-def test_qdense_ggml_not_implemented(host_backend):
-    _, f, x, w, s, _ = _qd_builder(host_backend, ca.Shape(ca.Float32, 1, 32), ca.Shape(ca.Uint8, 4, 18),
-                                   ca.Shape(ca.Float32, 1))
+def _ggml_q(t):
+    return ca.Quantization(ca.QuantGGML, None, None, 1, 1, int(t))
+
+
+def test_qdense_ggml_shape_and_validation(host_backend):
+    """FusedQuantizedDenseGGML's rules (quantizeddense.go:145-248)."""
+    b = host_backend
+    f = b.Builder("g").Main()
+    x = f.Parameter("x", ca.Shape(ca.Float32, 2, 3, 512))
+    w = f.Parameter("w", ca.Shape(ca.Uint8, 40, 512 // 32 * 18))
+    bias = f.Parameter("b", ca.Shape(ca.Float32, 40))
+    y = f.FusedQuantizedDense(x, w, bias, _ggml_q(ca.GGMLQ4_0), ca.ActivationGelu)
+    assert f.Shape(y) == ca.Shape(ca.Float32, 2, 3, 40)
+    wk = f.Parameter("wk", ca.Shape(ca.Uint8, 40, 2 * 210))
+    assert f.Shape(f.FusedQuantizedDense(x, wk, None, _ggml_q(ca.GGMLQ6_K), ca.ActivationNone)) == \
+        ca.Shape(ca.Float32, 2, 3, 40)
+    # unsupported block formats are NotImplemented (validateGGMLTypeSupported)
+    wq2 = f.Parameter("wq2", ca.Shape(ca.Uint8, 40, 2 * 84))
     with pytest.raises(ca.ErrNotImplemented):
-        f.FusedQuantizedDense(x, w, None, ca.Quantization(ca.QuantGGML, s, None, 1, 1), ca.ActivationNone)
+        f.FusedQuantizedDense(x, wq2, None, _ggml_q(ca.GGMLQ2_K), ca.ActivationNone)
+    bad = []
+    # bytesPerRow not a multiple of the block size, x not f32, K mismatch, zero point, bad bias
+    wodd = f.Parameter("wodd", ca.Shape(ca.Uint8, 40, 17))
+    bad.append(lambda: f.FusedQuantizedDense(x, wodd, None, _ggml_q(ca.GGMLQ4_0), ca.ActivationNone))
+    xb = f.Parameter("xb", ca.Shape(ca.BFloat16, 2, 512))
+    bad.append(lambda: f.FusedQuantizedDense(xb, w, None, _ggml_q(ca.GGMLQ4_0), ca.ActivationNone))
+    x2 = f.Parameter("x2", ca.Shape(ca.Float32, 2, 256))
+    bad.append(lambda: f.FusedQuantizedDense(x2, w, None, _ggml_q(ca.GGMLQ4_0), ca.ActivationNone))
+    zp = f.Parameter("zp", ca.Shape(ca.Float32, 40))
+    bad.append(lambda: f.FusedQuantizedDense(x, w, None, ca.Quantization(ca.QuantGGML, None, zp, 1, 1, 0),
+                                             ca.ActivationNone))
+    b2 = f.Parameter("b2", ca.Shape(ca.Float32, 41))
+    bad.append(lambda: f.FusedQuantizedDense(x, w, b2, _ggml_q(ca.GGMLQ4_0), ca.ActivationNone))
+    wi = f.Parameter("wi", ca.Shape(ca.Int8, 40, 288))
+    bad.append(lambda: f.FusedQuantizedDense(x, wi, None, _ggml_q(ca.GGMLQ4_0), ca.ActivationNone))
+    for call in bad:
+        with pytest.raises(ca.ComputeError) as ei:
+            call()
+        assert not ca.IsNotImplemented(ei.value)
+
+
+def test_quantized_embedding_lookup_shape_and_validation(host_backend):
+    """QuantizedEmbeddingLookup's rules (quantizeddense.go:266-321)."""
+    f = host_backend.Builder("e").Main()
+    data = f.Parameter("d", ca.Shape(ca.Uint8, 100, 2 * 34))
+    idx = f.Parameter("i", ca.Shape(ca.Int32, 2, 3, 1))
+    y = f.QuantizedEmbeddingLookup(data, idx, _ggml_q(ca.GGMLQ8_0))
+    assert f.Shape(y) == ca.Shape(ca.Float32, 2, 3, 64)
+    s = f.Parameter("s", ca.Shape(ca.Float32, 1))
+    with pytest.raises(ca.ErrNotImplemented):
+        f.QuantizedEmbeddingLookup(data, idx, ca.Quantization(ca.QuantLinear, s, None, 1, 1))
+    with pytest.raises(ca.ErrNotImplemented):
+        f.QuantizedEmbeddingLookup(data, idx, _ggml_q(ca.GGMLQ5_K))
+    i2 = f.Parameter("i2", ca.Shape(ca.Int32, 2, 3))
+    fi = f.Parameter("fi", ca.Shape(ca.Float32, 2, 1))
+    d3 = f.Parameter("d3", ca.Shape(ca.Uint8, 100, 2, 34))
+    for call in (lambda: f.QuantizedEmbeddingLookup(data, i2, _ggml_q(ca.GGMLQ8_0)),
+                 lambda: f.QuantizedEmbeddingLookup(data, fi, _ggml_q(ca.GGMLQ8_0)),
+                 lambda: f.QuantizedEmbeddingLookup(d3, idx, _ggml_q(ca.GGMLQ8_0)),
+                 lambda: f.QuantizedEmbeddingLookup(data, idx, _ggml_q(ca.GGMLQ4_0))):  # 68 % 18 != 0
+        with pytest.raises(ca.ComputeError) as ei:
+            call()
+        assert not ca.IsNotImplemented(ei.value)
 
 
 def test_values_from_other_builder_rejected(host_backend):

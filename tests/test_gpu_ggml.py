@@ -1,0 +1,176 @@
+"""GPU parity of the GGML block formats (compute_amd/csrc/ggml.hip) against the CPU oracle.
+
+- ggml_dense_exact (M > 4 rows, or anything the GEMV does not take): bit-identical f32 output,
+  bias and activation included (the reference's order: dot, then bias, then activation).
+- ggml_gemv (M <= 4): f32 accumulation bar — |y - exact| <= 1e-5 * sum|x*w| per output (the
+  kernel sums in another order), identical bits on repeated calls, rows whose byte length is
+  not a multiple of 16 (staging skew), the decode shape [1, 4096] x 11008 rows.
+- QuantizedEmbeddingLookup: bit-identical rows for every index dtype; an index outside
+  [0, vocab) fails the Execute call, as the reference's executor does.
+"""
+import numpy as np
+import pytest
+
+import compute_amd as ca
+from compute_amd import _lib
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [ca.GGMLQ4_0, ca.GGMLQ8_0, ca.GGMLIQ4NL, ca.GGMLQ4_K, ca.GGMLQ6_K]
+RNG = np.random.default_rng(7)
+
+
+class GgmlRun:
+    def __init__(self, backend, t, x, w, bias=None, act=ca.ActivationNone):
+        self.backend, self.t, self.act = backend, int(t), int(act)
+        self.M, self.K = x.shape
+        self.N, self.bpr = w.shape
+        bld = backend.Builder("ggml")
+        f = bld.Main()
+        shapes = [ca.Shape(ca.Float32, self.M, self.K), ca.Shape(ca.Uint8, self.N, self.bpr)]
+        datas = [x.astype(np.float32), w.astype(np.uint8)]
+        px = f.Parameter("x", shapes[0])
+        pw = f.Parameter("w", shapes[1])
+        pb = None
+        if bias is not None:
+            shapes.append(ca.Shape(ca.Float32, self.N))
+            datas.append(bias.astype(np.float32))
+            pb = f.Parameter("b", shapes[-1])
+        y = f.FusedQuantizedDense(px, pw, pb, ca.Quantization(ca.QuantGGML, None, None, 1, 1, self.t), act)
+        f.Return([y])
+        self.exe = bld.Compile()
+        self.inputs = [backend.BufferFromFlatData(0, d.ravel(), sh) for d, sh in zip(datas, shapes)]
+        self.has_bias = bias is not None
+
+    def plan(self):
+        a = _lib.mx_qdense_args()
+        a.x, a.w = self.inputs[0].DevicePtr(), self.inputs[1].DevicePtr()
+        a.out = self.inputs[0].DevicePtr()
+        if self.has_bias:
+            a.bias, a.bias_dtype = self.inputs[2].DevicePtr(), O.DT_FLOAT32
+        a.M, a.K, a.N = self.M, self.K, self.N
+        a.x_dtype, a.scheme, a.ggml_type, a.activation = O.DT_FLOAT32, int(ca.QuantGGML), self.t, self.act
+        return self.backend.QDensePlan(a)
+
+    def run(self):
+        out = self.exe.Execute(self.inputs)[0]
+        y = out.ToFlatData()
+        out.Finalize()
+        return y.reshape(self.M, self.N)
+
+
+def problem(t, M, K, N, bias=True):
+    w = O.ggml_random_rows(int(t), N, K, RNG)
+    x = RNG.standard_normal((M, K)).astype(np.float32)
+    b = RNG.standard_normal(N).astype(np.float32) if bias else None
+    return x, w, b
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("act", [ca.ActivationNone, ca.ActivationGelu, ca.ActivationSilu])
+def test_exact_kernel_bit_identical(backend, t, act):
+    x, w, b = problem(t, 6, 512, 72)
+    r = GgmlRun(backend, t, x, w, b, act)
+    assert r.plan() == "ggml_dense_exact"
+    got = r.run()
+    want = O.ggml_dense(x, w, int(t), b, int(act))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def accumulation_check(got, x, w, t, b, rel=1e-5):
+    exact, ab = O.ggml_dense_f64(x, w, int(t), b)
+    err = np.abs(got.astype(np.float64) - exact)
+    bound = rel * ab + 1e-30
+    assert (err <= bound).all(), f"worst {np.max(err / bound)} x the bound"
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_gemv_accumulation_bound(backend, t, M):
+    x, w, b = problem(t, M, 1024, 301)
+    r = GgmlRun(backend, t, x, w, b)
+    assert r.plan() == "ggml_gemv"
+    got = r.run()
+    accumulation_check(got, x, w, t, b)
+    assert np.array_equal(got.view(np.uint32), r.run().view(np.uint32))
+
+
+@pytest.mark.parametrize("t,K", [(ca.GGMLQ6_K, 256), (ca.GGMLQ8_0, 32), (ca.GGMLQ4_0, 96), (ca.GGMLQ4_K, 768)])
+def test_gemv_rows_not_16_byte_aligned(backend, t, K):
+    x, w, b = problem(t, 2, K, 37)
+    r = GgmlRun(backend, t, x, w, b)
+    assert r.plan() == "ggml_gemv"
+    accumulation_check(r.run(), x, w, t, b)
+
+
+@pytest.mark.parametrize("t", [ca.GGMLQ4_0, ca.GGMLQ4_K])
+def test_gemv_activation(backend, t):
+    x, w, b = problem(t, 1, 512, 64)
+    got = GgmlRun(backend, t, x, w, b, ca.ActivationGelu).run()
+    want = O.ggml_dense(x, w, int(t), b, int(ca.ActivationGelu))
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("t", [ca.GGMLQ4_0, ca.GGMLQ8_0, ca.GGMLQ4_K])
+def test_gemv_decode_shape(backend, t):
+    x, w, b = problem(t, 1, 4096, 11008, bias=False)
+    r = GgmlRun(backend, t, x, w, b)
+    assert r.plan() == "ggml_gemv"
+    accumulation_check(r.run(), x, w, t, b)
+
+
+def embed_graph(backend, t, data, idx, idx_dtype):
+    bld = backend.Builder("emb")
+    f = bld.Main()
+    ds = ca.Shape(ca.Uint8, *data.shape)
+    is_ = ca.Shape(idx_dtype, *idx.shape)
+    pd = f.Parameter("d", ds)
+    pi = f.Parameter("i", is_)
+    f.Return([f.QuantizedEmbeddingLookup(pd, pi, ca.Quantization(ca.QuantGGML, None, None, 1, 1, int(t)))])
+    exe = bld.Compile()
+    np_dt = {ca.Int32: np.int32, ca.Int64: np.int64, ca.Uint16: np.uint16, ca.Int8: np.int8}[idx_dtype]
+    ins = [backend.BufferFromFlatData(0, data.ravel(), ds),
+           backend.BufferFromFlatData(0, idx.astype(np_dt).ravel(), is_)]
+    return exe, ins
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("idx_dtype", [ca.Int32, ca.Int64, ca.Uint16, ca.Int8])
+def test_embedding_bit_identical(backend, t, idx_dtype):
+    V, K = 97, 512
+    data = O.ggml_random_rows(int(t), V, K, RNG)
+    idx = RNG.integers(0, V, (2, 3, 1))
+    idx[0, 0, 0] = V - 1
+    exe, ins = embed_graph(backend, t, data, idx, idx_dtype)
+    out = exe.Execute(ins)[0]
+    got = out.ToFlatData().reshape(2, 3, K)
+    out.Finalize()
+    want = O.ggml_embedding(data, int(t), idx).reshape(2, 3, K)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_embedding_out_of_range_fails_the_call(backend):
+    t, V, K = ca.GGMLQ8_0, 10, 64
+    data = O.ggml_random_rows(int(t), V, K, RNG)
+    for bad in (10, -1):
+        idx = np.array([[1], [bad], [2]])
+        exe, ins = embed_graph(backend, t, data, idx, ca.Int64)
+        with pytest.raises(ca.ComputeError, match=f"index {bad} out of range"):
+            exe.Execute(ins)
+
+
+def test_embedding_direct_entry_point(backend):
+    t, V, K = ca.GGMLQ4_K, 33, 1024
+    data = O.ggml_random_rows(int(t), V, K, RNG)
+    idx = RNG.integers(0, V, 17).astype(np.int32)
+    bd = backend.BufferFromFlatData(0, data.ravel(), ca.Shape(ca.Uint8, *data.shape))
+    bi = backend.BufferFromFlatData(0, idx, ca.Shape(ca.Int32, 17))
+    bo = backend.BufferFromFlatData(0, np.zeros(17 * K, np.float32), ca.Shape(ca.Float32, 17, K))
+    a = _lib.mx_qembed_args()
+    a.data, a.indices, a.out = bd.DevicePtr(), bi.DevicePtr(), bo.DevicePtr()
+    a.vocab, a.bytes_per_row, a.n = V, data.shape[1], 17
+    a.index_dtype, a.ggml_type = 4, int(t)  # Int32
+    backend.QEmbed(a)
+    got = bo.ToFlatData().reshape(17, K)
+    assert np.array_equal(got.view(np.uint32), O.ggml_embedding(data, int(t), idx).view(np.uint32))
