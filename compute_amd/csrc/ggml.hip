@@ -260,12 +260,14 @@ __device__ __forceinline__ void ggml_unit(const uint8_t* row, int u, const float
   }
 }
 
-template <int T, int MR>
-__global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d, int row_stride) {
+// CH: 16-byte chunks of a row per lane (the row, with its alignment skew, is at most 64*CH chunks).
+template <int T, int MR, int CH>
+__global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int kRowBytes = 64 * CH * 16;
   const int K = (int)d.K, units = K >> 5;
-  float* xs = (float*)lds;                                                  // [MR][units][kGvPad]
-  uint8_t* rows = lds + (size_t)MR * units * kGvPad * sizeof(float);        // [waves][row_stride]
+  float* xs = (float*)lds;                                             // [MR][units][kGvPad]
+  uint8_t* rows = lds + (size_t)MR * units * kGvPad * sizeof(float);   // [waves][kRowBytes]
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   for (int i = t; i < MR * K; i += kGvThreads) {
@@ -274,25 +276,33 @@ __global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d, int r
   }
   __syncthreads();
 
-  uint8_t* rb = rows + (size_t)wave * row_stride;
+  uint8_t* rb = rows + (size_t)wave * kRowBytes;
   // The weights are read in whole 16-byte units from a 16-byte-aligned base: the buffer's range
   // is its size rounded up to 16 (a partially valid unit must come back whole; the bytes past
   // the end lie in the same allocation granule, 256 bytes or more) and units beyond it read 0.
   const int64_t total = (d.N * d.bpr + 15) & ~(int64_t)15;
   const __amdgpu_buffer_rsrc_t wrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(d.w), (short)0, (int)total, 0x00020000);
-  for (int64_t n = (int64_t)blockIdx.x * kGvWaves + wave; n < d.N; n += (int64_t)gridDim.x * kGvWaves) {
-    // Stage the row: 16-byte loads from the aligned address at or below its start, the row then
-    // begins `skew` bytes into the buffer.
-    const int64_t base = n * d.bpr, a0 = base & ~(int64_t)15;
-    const int skew = (int)(base - a0);
-    const int nch = (int)((base + d.bpr - a0 + 15) >> 4);
-    for (int c = lane; c < nch; c += 64)
-      *(u32x4_v*)(rb + 16 * c) = __builtin_amdgcn_raw_buffer_load_b128(wrs, (unsigned)(a0 + 16 * c), 0, 0);
+  // A row is loaded into registers one row ahead (16-byte loads from the aligned address at or
+  // below its start; the row then begins `skew` bytes into the staging buffer), so its loads
+  // travel while the previous row is computed.
+  u32x4_v pre[CH];
+  auto issue = [&](int64_t row) {
+    const uint32_t a0 = (uint32_t)((min(row, d.N - 1) * d.bpr) & ~(int64_t)15);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) pre[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, a0 + 16u * (lane + 64 * i), 0, 0);
+  };
+  const int64_t stride = (int64_t)gridDim.x * kGvWaves;
+  int64_t n = (int64_t)blockIdx.x * kGvWaves + wave;
+  if (n < d.N) issue(n);
+  for (; n < d.N; n += stride) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) *(u32x4_v*)(rb + 16 * (lane + 64 * i)) = pre[i];
+    if (n + stride < d.N) issue(n + stride);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-    const uint8_t* row = rb + skew;
+    const uint8_t* row = rb + (int)((n * d.bpr) & 15);
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
@@ -322,31 +332,44 @@ __global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d, int r
   }
 }
 
-// LDS of the GEMV for these sizes, or 0 if it does not apply.
-static size_t ggml_gemv_lds(const GgmlDesc& d, int* row_stride) {
+// Chunks per lane (2, 4 or 8) and LDS of the GEMV for these sizes, or 0 if it does not apply.
+static size_t ggml_gemv_lds(const GgmlDesc& d, int* ch) {
   if (d.M < 1 || d.M > 4 || d.K % 32 != 0 || d.K > (1 << 20) || d.N * d.bpr + 16 >= ((int64_t)1 << 31) ||
       (uintptr_t)d.w % 16 != 0)
     return 0;
-  const int64_t rs = ((d.bpr + 15 + 15) / 16) * 16;
-  const size_t bytes = (size_t)d.M * (d.K / 32) * kGvPad * sizeof(float) + (size_t)kGvWaves * rs;
+  const int64_t chunks = (d.bpr + 15 + 15) / 16;  // worst-case skew included
+  int c = 2;
+  while (c < 8 && 64 * c < chunks) c *= 2;
+  if (64 * c < chunks) return 0;
+  const size_t bytes = (size_t)d.M * (d.K / 32) * kGvPad * sizeof(float) + (size_t)kGvWaves * 64 * c * 16;
   if (bytes > 150 * 1024) return 0;
-  *row_stride = (int)rs;
+  *ch = c;
   return bytes;
 }
 
 bool ggml_gemv_fits(const GgmlDesc& d) {
-  int rs;
-  return ggml_gemv_lds(d, &rs) != 0;
+  int ch;
+  return ggml_gemv_lds(d, &ch) != 0;
+}
+
+template <int T, int CH>
+static void launch_gemv_ch(const GgmlDesc& d, int grid, size_t lds, hipStream_t st) {
+  switch (d.M) {
+    case 1: dispatch(ggml_gemv_kernel<T, 1, CH>, grid, kGvThreads, lds, st, d); break;
+    case 2: dispatch(ggml_gemv_kernel<T, 2, CH>, grid, kGvThreads, lds, st, d); break;
+    case 3: dispatch(ggml_gemv_kernel<T, 3, CH>, grid, kGvThreads, lds, st, d); break;
+    default: dispatch(ggml_gemv_kernel<T, 4, CH>, grid, kGvThreads, lds, st, d); break;
+  }
 }
 
 template <int T>
-static void launch_gemv_t(const GgmlDesc& d, int grid, size_t lds, int rs, hipStream_t st) {
-  switch (d.M) {
-    case 1: dispatch(ggml_gemv_kernel<T, 1>, grid, kGvThreads, lds, st, d, rs); break;
-    case 2: dispatch(ggml_gemv_kernel<T, 2>, grid, kGvThreads, lds, st, d, rs); break;
-    case 3: dispatch(ggml_gemv_kernel<T, 3>, grid, kGvThreads, lds, st, d, rs); break;
-    default: dispatch(ggml_gemv_kernel<T, 4>, grid, kGvThreads, lds, st, d, rs); break;
-  }
+static void launch_gemv_t(const GgmlDesc& d, int grid, size_t lds, int ch, hipStream_t st) {
+  if (ch == 2)
+    launch_gemv_ch<T, 2>(d, grid, lds, st);
+  else if (ch == 4)
+    launch_gemv_ch<T, 4>(d, grid, lds, st);
+  else
+    launch_gemv_ch<T, 8>(d, grid, lds, st);
 }
 
 const char* ggml_plan_name(const GgmlDesc& d) {
@@ -358,17 +381,17 @@ int ggml_dense_run(mx_backend* b, const GgmlDesc& d) {
   MX_TRY(check_device(b));
   if (d.M == 0 || d.N == 0) return MX_OK;
   hipStream_t st = b->stream;
-  int rs = 0;
-  const size_t lds = ggml_gemv_lds(d, &rs);
+  int ch = 0;
+  const size_t lds = ggml_gemv_lds(d, &ch);
   if (lds) {
     const int grid = (int)std::min<int64_t>((d.N + kGvWaves - 1) / kGvWaves, 2 * (int64_t)std::max(b->num_cus, 1));
     return launch(b, "ggml_gemv", [&] {
       switch (d.type) {
-        case MX_GGML_Q4_0: launch_gemv_t<MX_GGML_Q4_0>(d, grid, lds, rs, st); break;
-        case MX_GGML_Q8_0: launch_gemv_t<MX_GGML_Q8_0>(d, grid, lds, rs, st); break;
-        case MX_GGML_IQ4_NL: launch_gemv_t<MX_GGML_IQ4_NL>(d, grid, lds, rs, st); break;
-        case MX_GGML_Q4_K: launch_gemv_t<MX_GGML_Q4_K>(d, grid, lds, rs, st); break;
-        default: launch_gemv_t<MX_GGML_Q6_K>(d, grid, lds, rs, st); break;
+        case MX_GGML_Q4_0: launch_gemv_t<MX_GGML_Q4_0>(d, grid, lds, ch, st); break;
+        case MX_GGML_Q8_0: launch_gemv_t<MX_GGML_Q8_0>(d, grid, lds, ch, st); break;
+        case MX_GGML_IQ4_NL: launch_gemv_t<MX_GGML_IQ4_NL>(d, grid, lds, ch, st); break;
+        case MX_GGML_Q4_K: launch_gemv_t<MX_GGML_Q4_K>(d, grid, lds, ch, st); break;
+        default: launch_gemv_t<MX_GGML_Q6_K>(d, grid, lds, ch, st); break;
       }
     });
   }

@@ -12,7 +12,7 @@ from typing import Optional
 import numpy as np
 
 from . import backend as B
-from .dtypes import BFloat16, DType, Float32, Int4, Int8, Shape, bf16_from_f32, pack_int4
+from .dtypes import BFloat16, DType, Float32, Int4, Int8, Shape, Uint8, bf16_from_f32, pack_int4
 
 
 @dataclass
@@ -135,6 +135,60 @@ class MLPWorkload:
         return sum(2 * self.M * K * N for _, _, K, N in self.weights)
 
 
+@dataclass
+class GGMLWorkload:
+    """FusedQuantizedDense over GGML block rows (not a BASELINE config; the SURVEY's next row):
+    f32 x [M, K], weights [N, bytesPerRow] Uint8 in one of the supported block formats."""
+
+    name: str
+    M: int
+    K: int
+    N: int
+    ggml_type: int
+    x: np.ndarray
+    w: np.ndarray
+
+    def shapes(self):
+        return [Shape(Float32, self.M, self.K), Shape(Uint8, *self.w.shape)]
+
+    def host_inputs(self):
+        return [self.x, self.w]
+
+    def compile(self, backend: B.Backend) -> B.Executable:
+        bld = backend.Builder(self.name)
+        f = bld.Main()
+        x, w = (f.Parameter(n, s) for n, s in zip(["x", "w"], self.shapes()))
+        q = B.Quantization(B.QuantGGML, None, None, 1, 1, self.ggml_type)
+        f.Return([f.FusedQuantizedDense(x, w, None, q, B.ActivationNone)])
+        return bld.Compile()
+
+    def upload(self, backend: B.Backend):
+        return [backend.BufferFromFlatData(0, d.ravel(), s) for d, s in zip(self.host_inputs(), self.shapes())]
+
+    def weight_bytes(self) -> int:
+        return self.w.nbytes
+
+    def algorithmic_bytes(self) -> int:
+        """Blocks read once (scales included), x read once, the f32 output written once."""
+        return self.x.nbytes + self.w.nbytes + self.M * self.N * 4
+
+    def flops(self) -> int:
+        return 2 * self.M * self.K * self.N
+
+
+def ggml_rows(t: int, n: int, k: int, rng) -> np.ndarray:
+    """Random GGML rows [n, bytesPerRow]: random codes, block scales (f16) in U(0.001, 0.02)."""
+    vpb, bpb = B.ggml_values_per_block(t), B.ggml_bytes_per_block(t)
+    nb = k // vpb
+    rows = rng.integers(0, 256, (n, nb, bpb), dtype=np.uint8)
+    offsets = {B.GGMLQ4_K: [0, 2], B.GGMLQ6_K: [208]}.get(t, [0])
+    for off in offsets:
+        d = rng.uniform(0.001, 0.02, (n, nb)).astype(np.float16).view(np.uint16)
+        rows[:, :, off] = d & 0xFF
+        rows[:, :, off + 1] = d >> 8
+    return rows.reshape(n, nb * bpb)
+
+
 def _rngs(seed: int, n: int):
     return [np.random.Generator(np.random.PCG64(s)) for s in np.random.SeedSequence(seed).spawn(n)]
 
@@ -182,4 +236,11 @@ def make(name: str, seed: int = 0) -> QDWorkload:
             sc = bf16_from_f32(rs.uniform(0.002, 0.02, (K // G, N)).astype(np.float32))
             ws.append((w, sc, K, N))
         return MLPWorkload("C5_mlp_int4_g128_batch8", M, D, F, G, x, ws)
+    ggml = {"G1": ("G1_ggml_q4_0_decode", B.GGMLQ4_0), "G2": ("G2_ggml_q4_k_decode", B.GGMLQ4_K),
+            "G3": ("G3_ggml_q8_0_decode", B.GGMLQ8_0), "G4": ("G4_ggml_q6_k_decode", B.GGMLQ6_K)}
+    if name in ggml:  # GGML decode GEMV at the C2 shape: x f32 [1,4096], 11008 block rows
+        label, t = ggml[name]
+        M, K, N = 1, 4096, 11008
+        x = rx.standard_normal((M, K)).astype(np.float32)
+        return GGMLWorkload(label, M, K, N, int(t), x, ggml_rows(int(t), N, K, rw))
     raise ValueError(f"unknown workload {name}")
