@@ -161,51 +161,69 @@ constexpr int kGvWaves = 8;
 constexpr int kGvThreads = 64 * kGvWaves;
 constexpr int kGvPad = 36;  // floats per 32-value unit of x in LDS
 
+// Four bytes of LDS at a 2-byte-aligned address.
+__device__ __forceinline__ uint32_t lds_dword2(const uint8_t* p) {
+  return (uint32_t)*(const uint16_t*)p | ((uint32_t)*(const uint16_t*)(p + 2) << 16);
+}
+
+// IQ4_NL table entries of four nibbles (one per byte of q), as four signed bytes: two byte
+// permutes over the 16-byte table (as int8), the high half chosen where bit 3 is set.
+__device__ __forceinline__ uint32_t iq4nl_bytes(uint32_t q) {
+  constexpr uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
+  const uint32_t sel = q & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+  const uint32_t m = ((q >> 3) & 0x01010101u) * 0xFFu;
+  return (hi & m) | (lo & ~m);
+}
+
 // Sum over one 32-value unit u of the row (starting at `row` in LDS) of x[m][32u + l] * w, for
-// each of the MR rows of x (xu[m] points at the unit in LDS).
+// each of the MR rows of x (xu[m] points at the unit in LDS, sx[m] is the unit's sum of x).  The
+// integer codes are converted four at a time (byte converts); a constant offset (Q4_0's -8,
+// Q4_K's min) is applied through sx.
 template <int T, int MR>
-__device__ __forceinline__ void ggml_unit(const uint8_t* row, int u, const float* const (&xu)[MR], float (&acc)[MR]) {
-  // x of the unit, 8 x 16 bytes per row of x.
+__device__ __forceinline__ void ggml_unit(const uint8_t* row, int u, const float* const (&xu)[MR], const float (&sx)[MR],
+                                          float (&acc)[MR]) {
   auto xv = [&](int m, int l) { return xu[m][l]; };
+  // s[m] += sum over the four bytes of `v` (unsigned codes) of x[m][l0 + b] * byte_b.
+  auto fma4u = [&](uint32_t v, int l0, float (&s)[MR]) {
+    const float q0 = (float)(v & 0xFFu), q1 = (float)((v >> 8) & 0xFFu);  // v_cvt_f32_ubyteN
+    const float q2 = (float)((v >> 16) & 0xFFu), q3 = (float)(v >> 24);
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      s[m] = fmaf(xv(m, l0 + 3), q3, fmaf(xv(m, l0 + 2), q2, fmaf(xv(m, l0 + 1), q1, fmaf(xv(m, l0), q0, s[m]))));
+  };
+  auto fma4s = [&](uint32_t v, int l0, float (&s)[MR]) {  // signed bytes
+    const float q0 = (float)(int8_t)v, q1 = (float)(int8_t)(v >> 8);
+    const float q2 = (float)(int8_t)(v >> 16), q3 = (float)(int8_t)(v >> 24);
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      s[m] = fmaf(xv(m, l0 + 3), q3, fmaf(xv(m, l0 + 2), q2, fmaf(xv(m, l0 + 1), q1, fmaf(xv(m, l0), q0, s[m]))));
+  };
+  float s[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) s[m] = 0.0f;
   if constexpr (T == MX_GGML_Q4_0 || T == MX_GGML_IQ4_NL) {
     const uint8_t* blk = row + 18 * u;
     const float d = f16_at(blk);
-    float s[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) s[m] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      const uint32_t two = *(const uint16_t*)(blk + 2 + j);
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t b = (two >> (8 * e)) & 0xFFu;
-        float lo, hi;
-        if constexpr (T == MX_GGML_Q4_0) {
-          lo = (float)((int)(b & 15u) - 8);
-          hi = (float)((int)(b >> 4) - 8);
-        } else {
-          lo = kIQ4NL[b & 15u];
-          hi = kIQ4NL[b >> 4];
-        }
-#pragma unroll
-        for (int m = 0; m < MR; ++m) s[m] = fmaf(xv(m, 16 + j + e), hi, fmaf(xv(m, j + e), lo, s[m]));
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v = lds_dword2(blk + 2 + 4 * i);
+      const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+      if constexpr (T == MX_GGML_Q4_0) {
+        fma4u(lo, 4 * i, s);
+        fma4u(hi, 16 + 4 * i, s);
+      } else {
+        fma4s(iq4nl_bytes(lo), 4 * i, s);
+        fma4s(iq4nl_bytes(hi), 16 + 4 * i, s);
       }
     }
 #pragma unroll
-    for (int m = 0; m < MR; ++m) acc[m] = fmaf(d, s[m], acc[m]);
+    for (int m = 0; m < MR; ++m) acc[m] = fmaf(d, T == MX_GGML_Q4_0 ? fmaf(-8.0f, sx[m], s[m]) : s[m], acc[m]);
   } else if constexpr (T == MX_GGML_Q8_0) {
     const uint8_t* blk = row + 34 * u;
     const float d = f16_at(blk);
-    float s[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) s[m] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; j += 2) {
-      const uint32_t two = *(const uint16_t*)(blk + 2 + j);
-      const float q0 = (float)(int8_t)(two & 0xFFu), q1 = (float)(int8_t)(two >> 8);
-#pragma unroll
-      for (int m = 0; m < MR; ++m) s[m] = fmaf(xv(m, j + 1), q1, fmaf(xv(m, j), q0, s[m]));
-    }
+    for (int i = 0; i < 8; ++i) fma4s(lds_dword2(blk + 2 + 4 * i), 4 * i, s);
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = fmaf(d, s[m], acc[m]);
   } else if constexpr (T == MX_GGML_Q4_K) {
@@ -216,19 +234,8 @@ __device__ __forceinline__ void ggml_unit(const uint8_t* row, int u, const float
     const float a = f16_at(blk) * (float)sc, b = f16_at(blk + 2) * (float)mn;
     const uint8_t* qs = blk + 16 + 32 * (jj >> 1);
     const int sh = 4 * (jj & 1);
-    float s[MR], sx[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) s[m] = sx[m] = 0.0f;
-#pragma unroll
-    for (int l = 0; l < 32; l += 2) {
-      const uint32_t two = *(const uint16_t*)(qs + l);
-      const float q0 = (float)((two >> sh) & 15u), q1 = (float)((two >> (8 + sh)) & 15u);
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        s[m] = fmaf(xv(m, l + 1), q1, fmaf(xv(m, l), q0, s[m]));
-        sx[m] += xv(m, l) + xv(m, l + 1);
-      }
-    }
+    for (int i = 0; i < 8; ++i) fma4u((lds_dword2(qs + 4 * i) >> sh) & 0x0F0F0F0Fu, 4 * i, s);
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = fmaf(a, s[m], fmaf(-b, sx[m], acc[m]));
   } else {  // MX_GGML_Q6_K: unit = quarter j of half h of a super-block
@@ -239,24 +246,18 @@ __device__ __forceinline__ void ggml_unit(const uint8_t* row, int u, const float
     const uint8_t* qh = blk + 128 + 32 * h;
     const int nsh = 4 * (j >> 1), hsh = 2 * j;
     const float sc0 = d * (float)(int8_t)blk[192 + 8 * h + 2 * j], sc1 = d * (float)(int8_t)blk[192 + 8 * h + 2 * j + 1];
-    float s0[MR], s1[MR];
+    float s1[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) s0[m] = s1[m] = 0.0f;
+    for (int m = 0; m < MR; ++m) s1[m] = 0.0f;
 #pragma unroll
-    for (int l = 0; l < 32; l += 2) {
-      const uint32_t lo2 = *(const uint16_t*)(ql + l), hi2 = *(const uint16_t*)(qh + l);
-      const float q0 = (float)((int)(((lo2 >> nsh) & 15u) | (((hi2 >> hsh) & 3u) << 4)) - 32);
-      const float q1 = (float)((int)(((lo2 >> (8 + nsh)) & 15u) | (((hi2 >> (8 + hsh)) & 3u) << 4)) - 32);
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        if (l < 16)
-          s0[m] = fmaf(xv(m, l + 1), q1, fmaf(xv(m, l), q0, s0[m]));
-        else
-          s1[m] = fmaf(xv(m, l + 1), q1, fmaf(xv(m, l), q0, s1[m]));
-      }
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t q = ((lds_dword2(ql + 4 * i) >> nsh) & 0x0F0F0F0Fu) | (((lds_dword2(qh + 4 * i) >> hsh) & 0x03030303u) << 4);
+      // Codes 0..63 stand for q - 32, the 6-bit two's complement value of q ^ 32: shifted into
+      // the top of each byte it reads as the signed byte 4 * (q - 32) (no carries between bytes).
+      fma4s((q ^ 0x20202020u) << 2, 4 * i, i < 4 ? s : s1);
     }
 #pragma unroll
-    for (int m = 0; m < MR; ++m) acc[m] = fmaf(sc0, s0[m], fmaf(sc1, s1[m], acc[m]));
+    for (int m = 0; m < MR; ++m) acc[m] = fmaf(0.25f * sc0, s[m], fmaf(0.25f * sc1, s1[m], acc[m]));
   }
 }
 
@@ -270,12 +271,6 @@ __global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d) {
   uint8_t* rows = lds + (size_t)MR * units * kGvPad * sizeof(float);   // [waves][kRowBytes]
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  for (int i = t; i < MR * K; i += kGvThreads) {
-    const int m = i / K, k = i - m * K;
-    xs[(m * units + (k >> 5)) * kGvPad + (k & 31)] = d.x[(size_t)m * K + k];
-  }
-  __syncthreads();
-
   uint8_t* rb = rows + (size_t)wave * kRowBytes;
   // The weights are read in whole 16-byte units from a 16-byte-aligned base: the buffer's range
   // is its size rounded up to 16 (a partially valid unit must come back whole; the bytes past
@@ -294,7 +289,22 @@ __global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d) {
   };
   const int64_t stride = (int64_t)gridDim.x * kGvWaves;
   int64_t n = (int64_t)blockIdx.x * kGvWaves + wave;
-  if (n < d.N) issue(n);
+  if (n < d.N) issue(n);  // before staging x: the first row travels meanwhile
+  for (int i = t; i < MR * K; i += kGvThreads) {
+    const int m = i / K, k = i - m * K;
+    xs[(m * units + (k >> 5)) * kGvPad + (k & 31)] = d.x[(size_t)m * K + k];
+  }
+  __syncthreads();
+  // Each unit's sum of x, kept in the unit's padding (slot 32), in a fixed order.
+  for (int i = t; i < MR * units; i += kGvThreads) {
+    float* xu = xs + (size_t)i * kGvPad;
+    float a = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) a += xu[l];
+    xu[32] = a;
+  }
+  __syncthreads();
+
   for (; n < d.N; n += stride) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) *(u32x4_v*)(rb + 16 * (lane + 64 * i)) = pre[i];
@@ -308,9 +318,13 @@ __global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d) {
     for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
     for (int u = lane; u < units; u += 64) {
       const float* xu[MR];
+      float sx[MR];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) xu[m] = xs + (size_t)(m * units + u) * kGvPad;
-      ggml_unit<T, MR>(row, u, xu, acc);
+      for (int m = 0; m < MR; ++m) {
+        xu[m] = xs + (size_t)(m * units + u) * kGvPad;
+        sx[m] = xu[m][32];
+      }
+      ggml_unit<T, MR>(row, u, xu, sx, acc);
     }
     // Lanes in a fixed tree.
 #pragma unroll
