@@ -83,6 +83,10 @@ struct Node {
   int64_t bpr = 0;  // GGML: bytes per weight row
   bool has_zp = false, has_bias = false;
   int res_op = 0;  // elementwise op folded into the epilogue (operand = last input)
+  // Pair (compile-time fusion of Mul(dense, dense) over one x): the second product's weights,
+  // scales and bias follow the first's inputs.
+  bool pair = false, has_bias2 = false;
+  int act2 = 0;
   int64_t M = 0, K = 0, N = 0;
   // DotNorm.
   int64_t B = 0;
@@ -1119,6 +1123,35 @@ static void fuse_dense_epilogues(const FunctionImpl& f, std::vector<Node>& nodes
   }
 }
 
+// FusedQuantizedDense whose folded Mul operand is another single-use FusedQuantizedDense over the
+// same x with the same shapes, scheme and dtypes (a gated MLP's up and gate projections): both
+// products run as one pair launch, out = round(round(up) * round(gate)), as the two kernels and
+// the folded Mul round it.
+static void fuse_dense_pairs(const FunctionImpl& f, std::vector<Node>& nodes) {
+  std::vector<int> uses = count_uses(f, nodes);
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    Node& n = nodes[i];
+    if (n.op != Op::kQDense || n.scheme == MX_QUANT_GGML || n.res_op != MX_OP_MUL || n.pair || n.has_zp) continue;
+    const int r = n.in.back();
+    const Node& g = nodes[r];
+    if (g.op != Op::kQDense || g.scheme != n.scheme || g.res_op != 0 || g.pair || g.has_zp || uses[r] != 1) continue;
+    if (g.in[0] != n.in[0] || g.M != n.M || g.K != n.K || g.N != n.N || g.shape != n.shape ||
+        g.block_axis != n.block_axis || g.block_size != n.block_size)
+      continue;
+    if (nodes[g.in[1]].shape != nodes[n.in[1]].shape || nodes[g.in[2]].shape != nodes[n.in[2]].shape) continue;
+    n.in.pop_back();
+    n.res_op = 0;
+    n.pair = true;
+    n.act2 = g.act;
+    n.has_bias2 = g.has_bias;
+    const std::vector<int> gin = g.in;
+    n.in.push_back(gin[1]);
+    n.in.push_back(gin[2]);
+    if (g.has_bias) n.in.push_back(gin[3]);
+    uses = count_uses(f, nodes);
+  }
+}
+
 // RMS normalisation written out with standard ops (as a GoMLX model builds it):
 //   xf = ConvertDType(x bf16 [M, D] -> f32); ss = ReduceSum(Mul(xf, xf), axis 1);
 //   t = Add(Mul(ss, c), e) with c, e f32 [M]; inv = Rsqrt(t);
@@ -1208,6 +1241,7 @@ int mx_builder_compile(mx_builder* bld, mx_executable** out) {
   if (!b->no_fusion) {
     fuse_rms_norm(bld->fn, e->nodes);
     fuse_dense_epilogues(bld->fn, e->nodes);
+    fuse_dense_pairs(bld->fn, e->nodes);
   }
   const int nn = (int)e->nodes.size();
 
@@ -1398,6 +1432,15 @@ static int run_node(mx_executable* e, int i, std::vector<void*>& ptr) {
         d.res_dt = ins((int)n.in.size() - 1).dtype;
         d.res_op = n.res_op;
       }
+      if (n.pair) {
+        int j = 3 + (n.has_zp ? 1 : 0) + (n.has_bias ? 1 : 0);
+        d.pair = true;
+        d.w2 = in(j);
+        d.scale2 = in(j + 1);
+        d.bias2 = n.has_bias2 ? in(j + 2) : nullptr;
+        d.b2_dt = n.has_bias2 ? ins(j + 2).dtype : 0;
+        d.act2 = n.act2;
+      }
       return qdense_run(b, d);
     }
     case Op::kDotNorm: {
@@ -1454,6 +1497,7 @@ extern "C" int mx_exec_describe(const mx_executable* e, char* buf, size_t buflen
     if (n.op == Op::kParameter || n.op == Op::kConstant || n.op == Op::kReshape || n.op == Op::kBitcast) continue;
     s += op_name(n.op);
     if (n.op == Op::kQDense && n.res_op) s += n.res_op == MX_OP_MUL ? "+Mul" : "+Add";
+    if (n.op == Op::kQDense && n.pair) s += "+Pair";
     s += "\n";
   }
   const size_t k = std::min(buflen - 1, s.size());

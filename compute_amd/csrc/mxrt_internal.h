@@ -112,6 +112,8 @@ struct mx_backend {
   int device = 0;
   bool host_only = false;
   bool no_fusion = false;  // "nofusion" option: compile graphs op by op
+  // "exact" option: FusedQuantizedDense always in the reference's loop order (bit-identical to it)
+  bool exact_qdense = false;
   bool finalized = false;
   hipStream_t stream = nullptr;
   std::recursive_mutex mu;
@@ -211,6 +213,14 @@ struct QDenseDesc {
   // MX_OP_MUL), rounded again as the separate elementwise op would.
   const void* res = nullptr;
   int res_dt = 0, res_op = 0;
+  // Pair: a second product over the same x with its own weights, scales, bias and activation
+  // (same shapes and dtypes), out = round(round(act(x.w + bias)) * round(act2(x.w2 + bias2))):
+  // the graph compiler's fusion of Mul(dense, dense) over one x (a gated MLP's gate and up).
+  bool pair = false;
+  const void* w2 = nullptr;
+  const void* scale2 = nullptr;
+  const void* bias2 = nullptr;
+  int b2_dt = 0, act2 = 0;
   // GGML scheme: block format (MX_GGML_*) and bytes per weight row ([N, bpr] storage).
   int ggml_type = 0;
   int64_t bpr = 0;
@@ -218,6 +228,9 @@ struct QDenseDesc {
 int qdense_validate(const mx_qdense_args* a, QDenseDesc* d);
 int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name);
 int qdense_run(mx_backend* b, const QDenseDesc& d);
+// Decode GEMV over the reference's own layouts (qdense_gemv.hip): shape/layout check and launch.
+bool qdense_gemv_fits(const QDenseDesc& d);
+int qdense_gemv_run(mx_backend* b, const QDenseDesc& d, const char* name);
 // Skinny-M MFMA kernel (qdense_skinny.hip): shape/layout check and launch.
 bool qdense_skinny_fits(const QDenseDesc& d);
 int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name);

@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kExactThreads) void qdense_exact_kernel(QDenseDesc 
 // =============================================================================================
 // Kernel selection.
 // =============================================================================================
-enum class QPath { kEmpty, kExact, kSkinny, kGemm };
+enum class QPath { kEmpty, kExact, kSkinny, kGemv, kGemm };
 
 static GgmlDesc ggml_desc(const QDenseDesc& d) {
   GgmlDesc g;
@@ -170,10 +170,11 @@ static GgmlDesc ggml_desc(const QDenseDesc& d) {
   return g;
 }
 
-static QPath choose_path(const QDenseDesc& d) {
+static QPath choose_path(const mx_backend* b, const QDenseDesc& d) {
   if (d.M == 0 || d.N == 0) return QPath::kEmpty;
-  if (d.scheme == MX_QUANT_GGML) return QPath::kExact;
+  if (d.scheme == MX_QUANT_GGML || b->exact_qdense) return QPath::kExact;
   if (qdense_skinny_fits(d)) return QPath::kSkinny;
+  if (qdense_gemv_fits(d)) return QPath::kGemv;
   if (qdense_gemm_fits(d)) return QPath::kGemm;
   return QPath::kExact;
 }
@@ -190,6 +191,14 @@ static const char* path_name(const QDenseDesc& d, QPath p) {
         case MX_DTYPE_INT8: return "qdense_skinny_mfma_i8";
         default: return "qdense_skinny_mfma_u8";
       }
+    case QPath::kGemv:
+      if (d.scheme == MX_QUANT_NF4) return dtype_is_packed(d.w_dt) ? "qdense_gemv_nf4_4bit" : "qdense_gemv_nf4_8bit";
+      switch (d.w_dt) {
+        case MX_DTYPE_INT4: return d.zp ? "qdense_gemv_i4_zp" : "qdense_gemv_i4";
+        case MX_DTYPE_UINT4: return d.zp ? "qdense_gemv_u4_zp" : "qdense_gemv_u4";
+        case MX_DTYPE_INT8: return d.zp ? "qdense_gemv_i8_zp" : "qdense_gemv_i8";
+        default: return d.zp ? "qdense_gemv_u8_zp" : "qdense_gemv_u8";
+      }
     default: return "qdense_exact";
   }
 }
@@ -200,13 +209,41 @@ int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name) {
     *name = ggml_plan_name(ggml_desc(d));
     return MX_OK;
   }
-  *name = path_name(d, choose_path(d));
+  const QPath p = choose_path(b, d);
+  *name = path_name(d, p);
+  if (d.pair) *name += p == QPath::kSkinny ? "_pair" : "+" + *name + "+mul";
   return MX_OK;
 }
 
 int qdense_run(mx_backend* b, const QDenseDesc& d) {
   MX_TRY(check_device(b));
-  const QPath p = choose_path(d);
+  const QPath p = choose_path(b, d);
+  if (d.pair && p != QPath::kSkinny && p != QPath::kEmpty) {
+    // Only the skinny kernel computes a pair in one launch: elsewhere the second product goes to
+    // a temporary and the first applies the product in its epilogue (the same arithmetic).
+    const size_t bytes = (size_t)d.M * d.N * (d.x_dt == MX_DTYPE_BFLOAT16 ? 2 : 4);
+    void* tmp = nullptr;
+    MX_TRY(dev_alloc(b, bytes, &tmp));
+    QDenseDesc d2 = d;
+    d2.pair = false;
+    d2.w = d.w2;
+    d2.scale = d.scale2;
+    d2.bias = d.bias2;
+    d2.b_dt = d.b2_dt;
+    d2.act = d.act2;
+    d2.out = tmp;
+    d2.res = nullptr;
+    d2.res_op = 0;
+    QDenseDesc d1 = d;
+    d1.pair = false;
+    d1.res = tmp;
+    d1.res_dt = d.x_dt;
+    d1.res_op = MX_OP_MUL;
+    int rc = qdense_run(b, d2);
+    if (rc == MX_OK) rc = qdense_run(b, d1);
+    dev_free(b, tmp);  // stream-ordered pool: later users run after these kernels
+    return rc;
+  }
   if (d.res_op != 0 && p != QPath::kSkinny && p != QPath::kEmpty) {
     // Only the skinny kernel applies a folded elementwise op in its epilogue: elsewhere the dense
     // result goes to a temporary and the op runs as its own kernel (the same arithmetic).
@@ -231,6 +268,8 @@ int qdense_run(mx_backend* b, const QDenseDesc& d) {
       return MX_OK;
     case QPath::kSkinny:
       return qdense_skinny_run(b, d, name);
+    case QPath::kGemv:
+      return qdense_gemv_run(b, d, name);
     case QPath::kGemm:
       return qdense_gemm_run(b, d, name);
     default: {

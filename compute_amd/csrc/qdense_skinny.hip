@@ -66,7 +66,13 @@ struct SkinnyArgs {
   float* partial;       // [S, M, N] (S > 1)
   uint32_t* counters;   // [column blocks], zero between launches
   const void* res;      // [M, N] epilogue operand (res_op != 0)
+  // Pair mode: a second product over the same x (w2, scale2, bias2, act2: same shapes and
+  // dtypes), out = round(round(act(y + bias)) * round(act2(y2 + bias2))).
+  const uint8_t* w2;
+  const void* scale2;
+  const void* bias2;
   int M, K, N, G, S, act, s_dt, b_dt, res_dt, res_op;
+  int pair, act2, b2_dt;
 };
 
 __device__ __forceinline__ f32x4_t sk_mfma(const u32x4_v& a, const u32x4_v& b, f32x4_t c) {
@@ -128,7 +134,12 @@ qdense_skinny_kernel(SkinnyArgs a) {
   __shared__ int s_last;
 
   const int item = sk_xcd_swizzle(blockIdx.x, gridDim.x);
-  const int cb = item / a.S, slice = item % a.S;
+  // Work items of a column block are consecutive: [matrix (pair mode)][slice].
+  const int SP = a.pair ? 2 * a.S : a.S;  // partial tiles per column block
+  const int cb = item / SP, part = item % SP;
+  const int mat = part >= a.S ? 1 : 0, slice = part - mat * a.S;
+  const uint8_t* wmat = mat ? a.w2 : a.w;
+  const void* smat = mat ? a.scale2 : a.scale;
   // The wave index is wave-uniform; saying so keeps the control flow scalar.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int cg = lane & 15, kq = lane >> 4;
@@ -149,11 +160,11 @@ qdense_skinny_kernel(SkinnyArgs a) {
     // Lanes whose columns lie past N read column 0 instead (their results are never stored).
     const size_t row_bytes = kI4 ? (size_t)(a.N >> 1) : (size_t)a.N;
     const size_t lbyte = (kI4 ? (size_t)(col0 >> 1) : (size_t)col0);
-    const uint8_t* wp = a.w + (size_t)(32 * wb + 8 * kq) * row_bytes + (lbyte + kSkLaneBytes <= row_bytes ? lbyte : 0);
+    const uint8_t* wp = wmat + (size_t)(32 * wb + 8 * kq) * row_bytes + (lbyte + kSkLaneBytes <= row_bytes ? lbyte : 0);
     const uint16_t* xp = a.x + (size_t)min(cg, a.M - 1) * a.K + 32 * wb + 8 * kq;
     const int sb = a.s_dt == MX_DTYPE_BFLOAT16 ? 2 : 4;
     const int scol = col0 < a.N ? col0 : 0;
-    const char* sp = (const char*)a.scale + (size_t)scol * sb;
+    const char* sp = (const char*)smat + (size_t)scol * sb;
     const int s_last_load = CPL * sb / 16 - 1;
 
     // Per scale group: its steps' x and weights, then its scales (needed only after its last
@@ -282,8 +293,9 @@ qdense_skinny_kernel(SkinnyArgs a) {
   constexpr int kMaxQuads = kSkMaxRows * kQPR / kSkThreads;           // quads per thread (M = 16)
   const int t = threadIdx.x;
   const int MC = M * kCols, NQ = M * kQPR;
-  // Epilogue operands of a quad (bias, folded elementwise operand), loaded unconditionally
-  // (clamped into range) so that they travel with the loads they are issued beside.
+  // Epilogue operands of a quad (bias, and the folded elementwise operand or the pair's second
+  // bias), loaded unconditionally (clamped into range) so that they travel with the loads they
+  // are issued beside.
   struct QuadOps {
     SkWord b[4], r[4];
   };
@@ -293,19 +305,23 @@ qdense_skinny_kernel(SkinnyArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       q.b[e] = sk_word(a.bias, c + e, a.b_dt, a.x);
-      q.r[e] = sk_word(a.res_op ? a.res : nullptr, (size_t)m * a.N + c + e, a.res_dt, a.x);
+      q.r[e] = a.pair ? sk_word(a.bias2, c + e, a.b2_dt, a.x)
+                      : sk_word(a.res_op ? a.res : nullptr, (size_t)m * a.N + c + e, a.res_dt, a.x);
     }
     return q;
   };
-  // bias, activation, bf16, the folded elementwise op (rounded as the separate op rounds it), and
-  // one 8-byte store of the quad.
-  auto finish_quad = [&](int m, int col, f32x4_t y, const QuadOps& q) {
+  // bias, activation, bf16, the folded elementwise op or the pair product (each rounded as the
+  // separate ops round it), and one 8-byte store of the quad.
+  auto finish_quad = [&](int m, int col, f32x4_t y, f32x4_t y2, const QuadOps& q) {
     if (col >= a.N) return;
     uint16_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       o[e] = f32_to_bf16(act_fast(y[e] + sk_value(q.b[e], a.bias, a.b_dt), a.act));
-      if (a.res_op) {
+      if (a.pair) {
+        const uint16_t g = f32_to_bf16(act_fast(y2[e] + sk_value(q.r[e], a.bias2, a.b2_dt), a.act2));
+        o[e] = f32_to_bf16(mul_rn(bf16_to_f32(o[e]), bf16_to_f32(g)));
+      } else if (a.res_op) {
         const float v = bf16_to_f32(o[e]), r = sk_value(q.r[e], a.res, a.res_dt);
         o[e] = f32_to_bf16(a.res_op == MX_OP_MUL ? mul_rn(v, r) : add_rn(v, r));
       }
@@ -313,7 +329,7 @@ qdense_skinny_kernel(SkinnyArgs a) {
     *(u32x2_v*)(a.out + (size_t)m * a.N + col) = u32x2_v{o[0] | (uint32_t)o[1] << 16, o[2] | (uint32_t)o[3] << 16};
   };
 
-  if (a.S == 1) {
+  if (SP == 1) {
     QuadOps ops[kMaxQuads];
 #pragma unroll
     for (int i = 0; i < kMaxQuads; ++i) {
@@ -328,19 +344,19 @@ qdense_skinny_kernel(SkinnyArgs a) {
         f32x4_t y = *(const f32x4_t*)(red + 4 * g);
 #pragma unroll
         for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
-        finish_quad(g / kQPR, cblk + 4 * (g % kQPR), y, ops[i]);
+        finish_quad(g / kQPR, cblk + 4 * (g % kQPR), y, y, ops[i]);
       }
     }
     return;
   }
   __syncthreads();
 
-  // Split K: store this slice's tile as [slice][M][N] (16-byte stores with the agent-scope
-  // coherence bit sc1: visible across the XCDs' L2s without whole-cache maintenance), wait until
-  // the stores have completed, then count the arrival.  Only the last arriver reads the tiles
-  // back, with loads that carry the same bit.
+  // Split K (or pair mode): store this work item's tile as [matrix][slice][M][N] (16-byte stores
+  // with the agent-scope coherence bit sc1: visible across the XCDs' L2s without whole-cache
+  // maintenance), wait until the stores have completed, then count the arrival.  Only the last
+  // arriver reads the tiles back, with loads that carry the same bit.
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-      a.partial, (short)0, (int)((size_t)a.S * M * a.N * sizeof(float)), 0x00020000);
+      a.partial, (short)0, (int)((size_t)SP * M * a.N * sizeof(float)), 0x00020000);
   constexpr int kSc1 = 16;  // cache-policy operand of the buffer intrinsics: sc1
 #pragma unroll
   for (int i = 0; i < kMaxQuads; ++i) {
@@ -351,41 +367,47 @@ qdense_skinny_kernel(SkinnyArgs a) {
 #pragma unroll
       for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, y), prs,
-                                            (unsigned)(((slice * M + m) * a.N + col) * 4), 0, kSc1);
+                                            (unsigned)(((part * M + m) * a.N + col) * 4), 0, kSc1);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(&a.counters[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == (uint32_t)a.S - 1u;
+    const int last = prev == (uint32_t)SP - 1u;
     if (last) __hip_atomic_store(&a.counters[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last;
   }
   __syncthreads();
   if (!s_last) return;
-  // Last arriver: each quad's S partial tiles, kSl slices per batch of loads (all in flight
-  // together), added in slice order.
+  // Last arriver: each quad's SP partial tiles, kSl per batch of loads (all in flight together),
+  // added in slice order per matrix (from 0 when S > 1, as the split single product adds them;
+  // a pair with S = 1 takes each matrix's one tile as it is, as the unsplit kernel does).
   constexpr int kSl = 16;
   for (int g = t; g < NQ; g += kSkThreads) {
     const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
     const int c = min(col, a.N - 4);
-    f32x4_t y = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4_t y = {0.0f, 0.0f, 0.0f, 0.0f}, y2 = y;
     QuadOps ops;
-    for (int s0 = 0; s0 < a.S; s0 += kSl) {
+    for (int s0 = 0; s0 < SP; s0 += kSl) {
       f32x4_t v[kSl];
 #pragma unroll
       for (int u = 0; u < kSl; ++u) {
-        const int s = min(s0 + u, a.S - 1);
+        const int s = min(s0 + u, SP - 1);
         v[u] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                prs, (unsigned)(((s * M + m) * a.N + c) * 4), 0, kSc1));
       }
       if (s0 == 0) ops = quad_ops(m, col);
 #pragma unroll
-      for (int u = 0; u < kSl; ++u)
-        if (s0 + u < a.S) y += v[u];
+      for (int u = 0; u < kSl; ++u) {
+        const int s = s0 + u;
+        if (s < a.S)
+          y = a.S == 1 ? v[u] : y + v[u];
+        else if (s < SP)
+          y2 = a.S == 1 ? v[u] : y2 + v[u];
+      }
     }
-    finish_quad(m, col, y, ops);
+    finish_quad(m, col, y, y2, ops);
   }
 }
 
@@ -398,7 +420,8 @@ bool qdense_skinny_fits(const QDenseDesc& d) {
   return d.M >= 1 && d.M <= kSkMaxRows && d.x_dt == MX_DTYPE_BFLOAT16 && d.scheme == MX_QUANT_LINEAR && !d.zp &&
          d.block_axis == 0 && d.K >= 32 && d.K % 32 == 0 && G % 32 == 0 && d.N >= 16 &&
          d.N % (dtype_is_packed(d.w_dt) ? 32 : 16) == 0 && d.K < (int64_t)1 << 30 && d.N < (int64_t)1 << 30 &&
-         aligned(d.w, 16) && aligned(d.x, 16) && aligned(d.scale, 16) && aligned(d.out, 8);
+         aligned(d.w, 16) && aligned(d.x, 16) && aligned(d.scale, 16) && aligned(d.out, 8) &&
+         (!d.pair || (aligned(d.w2, 16) && aligned(d.scale2, 16) && d.res_op == 0));
 }
 
 // Steps per wave T and steps per scale group seen by a wave FL (FL divides T and the steps of a
@@ -448,8 +471,9 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   const SkSteps sp = skinny_steps(d);
   const int64_t chunks = d.K / 32 / sp.T;  // wave-sized pieces of one column block
   const int64_t S = (chunks + kSkWaves - 1) / kSkWaves;
+  const int64_t SP = d.pair ? 2 * S : S;  // partial tiles per column block
   const size_t counter_bytes = 64 * 1024;
-  if ((size_t)nb * 4 > counter_bytes || nb * S > (int64_t)1 << 30 || S * d.M * d.N * 4 >= (int64_t)1 << 31)
+  if ((size_t)nb * 4 > counter_bytes || nb * SP > (int64_t)1 << 30 || SP * d.M * d.N * 4 >= (int64_t)1 << 31)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: N=%lld too large for the skinny path", (long long)d.N);
   SkinnyArgs ga;
   ga.x = (const uint16_t*)d.x;
@@ -459,9 +483,9 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.out = (uint16_t*)d.out;
   ga.partial = nullptr;
   ga.counters = nullptr;
-  if (S > 1) {
+  if (SP > 1) {
     void* scratch = nullptr;
-    MX_TRY(ensure_scratch(b, counter_bytes + (size_t)S * d.M * d.N * sizeof(float), &scratch));
+    MX_TRY(ensure_scratch(b, counter_bytes + (size_t)SP * d.M * d.N * sizeof(float), &scratch));
     ga.counters = (uint32_t*)scratch;
     ga.partial = (float*)((char*)scratch + counter_bytes);
   }
@@ -476,7 +500,13 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.res = d.res;
   ga.res_dt = d.res_dt;
   ga.res_op = d.res_op;
-  const int grid = (int)(nb * S);
+  ga.w2 = (const uint8_t*)d.w2;
+  ga.scale2 = d.scale2;
+  ga.bias2 = d.bias2;
+  ga.pair = d.pair ? 1 : 0;
+  ga.act2 = d.act2;
+  ga.b2_dt = d.b2_dt;
+  const int grid = (int)(nb * SP);
   // LDS: the waves' tiles [waves][M][cols].
   const size_t lds = (size_t)kSkWaves * d.M * cols * sizeof(float);
   hipStream_t st = b->stream;

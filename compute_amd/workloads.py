@@ -12,7 +12,7 @@ from typing import Optional
 import numpy as np
 
 from . import backend as B
-from .dtypes import BFloat16, DType, Float32, Int4, Int8, Shape, Uint8, bf16_from_f32, pack_int4
+from .dtypes import BFloat16, DType, Float32, Int4, Int8, Shape, Uint4, Uint8, bf16_from_f32, pack_int4
 
 
 @dataclass
@@ -33,6 +33,7 @@ class QDWorkload:
     w: np.ndarray
     scale: np.ndarray
     bias: Optional[np.ndarray]
+    scheme: int = int(B.QuantLinear)
 
     def shapes(self):
         s = [Shape(self.x_dtype, self.M, self.K), Shape(self.w_dtype, self.K, self.N),
@@ -52,7 +53,7 @@ class QDWorkload:
         f = bld.Main()
         params = [f.Parameter(n, s) for n, s in zip(["x", "w", "scale", "bias"], self.shapes())]
         bias = params[3] if self.bias is not None else None
-        q = B.Quantization(B.QuantLinear, params[2], None, self.block_axis, self.block_size)
+        q = B.Quantization(B.QuantizationScheme(self.scheme), params[2], None, self.block_axis, self.block_size)
         y = f.FusedQuantizedDense(params[0], params[1], bias, q, B.ActivationType(self.act))
         f.Return([y])
         return bld.Compile()
@@ -236,6 +237,15 @@ def make(name: str, seed: int = 0) -> QDWorkload:
             sc = bf16_from_f32(rs.uniform(0.002, 0.02, (K // G, N)).astype(np.float32))
             ws.append((w, sc, K, N))
         return MLPWorkload("C5_mlp_int4_g128_batch8", M, D, F, G, x, ws)
+    if name in ("R1", "R2"):  # the reference's own layout at the C2 shape: f32 x, scale [K, N/128]
+        M, K, N, G = 1, 4096, 11008, 128
+        nf4 = name == "R2"
+        x = rx.standard_normal((M, K)).astype(np.float32)
+        w = pack_int4(rw.integers(0, 16, K * N) if nf4 else rw.integers(-8, 8, K * N))
+        s = rs.uniform(0.002, 0.02, (K, (N + G - 1) // G)).astype(np.float32)
+        label = "R2_ref_layout_decode_nf4_f32" if nf4 else "R1_ref_layout_decode_int4_f32"
+        return QDWorkload(label, M, K, N, Float32, Uint4 if nf4 else Int4, Float32, s.shape, 1, G, None, 0, x, w, s,
+                          None, scheme=int(B.QuantNF4) if nf4 else int(B.QuantLinear))
     ggml = {"G1": ("G1_ggml_q4_0_decode", B.GGMLQ4_0), "G2": ("G2_ggml_q4_k_decode", B.GGMLQ4_K),
             "G3": ("G3_ggml_q8_0_decode", B.GGMLQ8_0), "G4": ("G4_ggml_q6_k_decode", B.GGMLQ6_K)}
     if name in ggml:  # GGML decode GEMV at the C2 shape: x f32 [1,4096], 11008 block rows

@@ -149,8 +149,11 @@ typedef uint64_t mx_value;
  * ------------------------------------------------------------------------------------------- */
 
 /* Constructor registered as "mi355x" (compute.go:129 Register / :220 NewWithConfig).
- * config: "" | "device=N" | "host_only" (graph building and shape checks only; every device
- * operation then fails with MX_ERR_NO_DEVICE). */
+ * config: comma-separated options: "device=N"; "host_only" (graph building and shape checks
+ * only; every device operation then fails with MX_ERR_NO_DEVICE); "nofusion" (compile graphs op
+ * by op); "exact" (FusedQuantizedDense always in the reference's loop order, bit-identical to
+ * quantizeddense.go:586-650 at every size; without it, decode and prefill shapes take the fast
+ * kernels, which differ only in summation order). */
 int mx_backend_new(const char* config, mx_backend** out);
 /* Backend.Finalize (compute.go:95). Frees all device memory; later calls fail MX_ERR_FINALIZED. */
 int mx_backend_finalize(mx_backend* b);

@@ -10,7 +10,7 @@ import pytest
 import compute_amd as ca
 from compute_amd import backend as B
 from compute_amd import workloads
-from compute_amd.dtypes import BFloat16, Float32, Int4, Int8, Shape, bf16_from_f32, pack_int4
+from compute_amd.dtypes import BFloat16, Float32, Int4, Int8, Shape, Uint4, Uint8, bf16_from_f32, pack_int4
 from tests.qd_helpers import assert_bf16_close
 from oracle import oracle as O
 
@@ -27,8 +27,7 @@ def host():
 
 def test_mlp_fused_ops(host):
     wl = workloads.make("C5")
-    assert wl.compile(host).Describe() == ['RmsNorm', 'FusedQuantizedDense', 'FusedQuantizedDense+Mul',
-                                           'FusedQuantizedDense+Add']
+    assert wl.compile(host).Describe() == ['RmsNorm', 'FusedQuantizedDense+Pair', 'FusedQuantizedDense+Add']
 
 
 def test_nofusion_option():
@@ -139,3 +138,100 @@ def test_dense_epilogue_equals_unfused(backend, x_dtype, op, res_first):
     finally:
         nf.Finalize()
     assert np.array_equal(outs[0], outs[1])
+
+
+# ---------------------------------------------------------------------------------------------
+# Pair fusion: Mul(dense(x, w_gate), dense(x, w_up)) over one x runs as one launch.
+# ---------------------------------------------------------------------------------------------
+def _pair_data(M, K, N, wdt, G, bias_g, bias_u, x_dtype, seed):
+    rng = np.random.default_rng(seed)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    x = bf16_from_f32(xs) if x_dtype == BFloat16 else xs
+    packed = wdt in (Int4, Uint4)
+    lo, hi = {Int4: (-8, 8), Uint4: (0, 16), Int8: (-127, 128), Uint8: (0, 256)}[wdt]
+    ng = 1 if G >= K else K // G
+    sdims = (N,) if G >= K else (ng, N)
+
+    def weights():
+        v = rng.integers(lo, hi, (K, N))
+        return pack_int4(v) if packed else v.astype(np.int8 if wdt == Int8 else np.uint8)
+
+    def scales():
+        return bf16_from_f32(rng.uniform(0.002, 0.02, sdims).astype(np.float32))
+
+    def bias():
+        return bf16_from_f32((rng.standard_normal(N) * 0.05).astype(np.float32))
+
+    data = {"x": x, "wg": weights(), "sg": scales(), "wu": weights(), "su": scales()}
+    if bias_g:
+        data["bg"] = bias()
+    if bias_u:
+        data["bu"] = bias()
+    shapes = {"x": Shape(x_dtype, M, K), "wg": Shape(wdt, K, N), "sg": Shape(BFloat16, *sdims),
+              "wu": Shape(wdt, K, N), "su": Shape(BFloat16, *sdims), "bg": Shape(BFloat16, N),
+              "bu": Shape(BFloat16, N)}
+    return data, shapes
+
+
+def _pair_graph(backend, data, shapes, G, act_g, act_u, gate_first=True, gate_output=False, other_x=False):
+    bld = backend.Builder("pair")
+    f = bld.Main()
+    p = {k: f.Parameter(k, shapes[k]) for k in data}
+    xg = p["x"]
+    if other_x:
+        xg = f.ConvertDType(f.ConvertDType(p["x"], Float32), shapes["x"].dtype)
+
+    def qd(x, w, s, b, act):
+        return f.FusedQuantizedDense(x, p[w], p.get(b), B.Quantization(B.QuantLinear, p[s], None, 0, G),
+                                     B.ActivationType(act))
+
+    g = qd(xg, "wg", "sg", "bg", act_g)
+    u = qd(p["x"], "wu", "su", "bu", act_u)
+    y = f.Mul(g, u) if gate_first else f.Mul(u, g)
+    f.Return([y, g] if gate_output else [y])
+    return bld.Compile()
+
+
+def test_pair_fusion_rules(host):
+    data, shapes = _pair_data(2, 256, 64, Int8, 64, False, True, BFloat16, 0)
+    silu, none = int(B.ActivationSilu), int(B.ActivationNone)
+    assert _pair_graph(host, data, shapes, 64, silu, none).Describe() == ["FusedQuantizedDense+Pair"]
+    assert _pair_graph(host, data, shapes, 64, silu, none, gate_first=False).Describe() == [
+        "FusedQuantizedDense+Pair"]
+    # The gate is also an output: it must exist on its own, so only the Mul is folded.
+    assert _pair_graph(host, data, shapes, 64, silu, none, gate_output=True).Describe() == [
+        "FusedQuantizedDense", "FusedQuantizedDense+Mul"]
+    # Different x operands: no pair.
+    assert "FusedQuantizedDense+Pair" not in _pair_graph(host, data, shapes, 64, silu, none, other_x=True).Describe()
+
+
+PAIR_CASES = [
+    # M, K, N, wdt, G, bias_g, bias_u, x_dtype
+    (1, 4096, 512, Int4, 128, False, False, BFloat16),   # S = 4 slices per matrix
+    (8, 4096, 768, Int4, 128, False, False, BFloat16),   # the C5 shape family (batch 8)
+    (3, 1024, 256, Uint4, 1024, True, False, BFloat16),  # per-channel scales, S = 1
+    (16, 2048, 384, Int8, 64, True, True, BFloat16),     # int8 g64, both biases
+    (5, 512, 160, Uint8, 512, False, True, BFloat16),    # S = 1, ragged column block
+    (4, 256, 64, Int8, 64, True, True, Float32),         # f32 x: exact kernels, pair fallback
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", PAIR_CASES, ids=lambda c: f"M{c[0]}K{c[1]}N{c[2]}_{c[3].name}_g{c[4]}")
+def test_pair_equals_unfused(backend, case):
+    M, K, N, wdt, G, bias_g, bias_u, x_dtype = case
+    data, shapes = _pair_data(M, K, N, wdt, G, bias_g, bias_u, x_dtype, seed=M * 131 + K)
+    nf = ca.New("nofusion")
+    try:
+        outs = []
+        for b, gate_first in ((backend, True), (backend, False), (nf, True)):
+            e = _pair_graph(b, data, shapes, G, int(B.ActivationSilu), int(B.ActivationNone), gate_first)
+            if b is backend:
+                assert e.Describe() == ["FusedQuantizedDense+Pair"]
+            bufs = [b.BufferFromFlatData(0, data[k], shapes[k]) for k in data]
+            outs.append(e.Execute(bufs)[0].ToFlatData())
+            outs.append(e.Execute(bufs)[0].ToFlatData())  # a second launch reuses the counters
+    finally:
+        nf.Finalize()
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)

@@ -1,0 +1,128 @@
+"""Decode GEMV over the reference's own layouts (qdense_gemv.hip) vs the CPU oracle.
+
+The reference's FusedQuantizedDense takes f32 x and scales in its own layout, scale[k, n/B]
+(BlockAxis = 1, quantizeddense.go:111-123), with Linear (optionally with a zero point) or NF4
+dequantisation.  Small problems keep the reference-order kernel (bit-identical); at decode sizes
+(K*N >= 2^20, M <= 4) the GEMV kernel runs, whose results differ from the reference loop only by
+summation order and the folding of the scale into x:
+  - f32 outputs: within 1e-5 of sum|terms| of the f64 value (the north star's fp32 bar);
+  - bf16 outputs: within rel 1e-2 / abs 1e-3 of the oracle's f32 result, and the same
+    accumulation bound plus half a bf16 ulp.
+"""
+import numpy as np
+import pytest
+
+import compute_amd as ca
+from oracle import oracle as O
+from tests.qd_helpers import QDenseRun, assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+
+W_DTYPES = [O.DT_INT8, O.DT_UINT8, O.DT_INT4, O.DT_UINT4]
+
+
+def _check(p, y, act_slack=1.0):
+    truth = O.qdense_f64(p)
+    scale = O.qdense_f64(p, absolute=True)
+    ref = O.qdense_f32(p)
+    if p.x_dtype == O.DT_FLOAT32:
+        if p.act == O.ACT_NONE:
+            assert np.all(np.abs(y.astype(np.float64) - truth) <= 1e-5 * scale + 1e-30), "f32 accumulation bound"
+        else:
+            err = np.abs(y.astype(np.float64) - ref.astype(np.float64))
+            assert np.all(err <= act_slack * 1e-5 * scale + 1e-6 * np.abs(ref)), "f32 bound through the activation"
+    else:
+        assert_bf16_close(y, ref)
+        if p.act == O.ACT_NONE:
+            got = O.bf16_to_f32(y).astype(np.float64)
+            assert np.all(np.abs(got - truth) <= 2.0 ** -8 * np.abs(truth) + 1e-5 * scale)
+
+
+def _run(backend, p, expect="qdense_gemv"):
+    r = QDenseRun(backend, p)
+    assert r.plan().startswith(expect), r.plan()
+    return r, r.run()
+
+
+@pytest.mark.parametrize("w_dtype", W_DTYPES)
+@pytest.mark.parametrize("zp", [False, True])
+@pytest.mark.parametrize("M", [1, 3])
+def test_gemv_linear_f32(backend, w_dtype, zp, M):
+    p = O.make_problem(M, 1024, 1024, w_dtype=w_dtype, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32,
+                       block_axis=1, block_size=64, bias=True, zp=zp, seed=100 + M * 10 + w_dtype)
+    r, y = _run(backend, p)
+    assert r.plan().endswith("_zp") == zp
+    _check(p, y)
+
+
+@pytest.mark.parametrize("w_dtype", [O.DT_UINT8, O.DT_INT8, O.DT_INT4, O.DT_UINT4])
+@pytest.mark.parametrize("M", [1, 4])
+def test_gemv_nf4(backend, w_dtype, M):
+    p = O.make_problem(M, 1024, 1536, w_dtype=w_dtype, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32,
+                       block_axis=1, block_size=128, bias=M == 1, scheme=O.QUANT_NF4, seed=200 + M + w_dtype)
+    r, y = _run(backend, p, "qdense_gemv_nf4")
+    _check(p, y)
+
+
+@pytest.mark.parametrize("w_dtype", W_DTYPES)
+@pytest.mark.parametrize("scale_dtype", [O.DT_BFLOAT16, O.DT_FLOAT32])
+def test_gemv_bf16_x(backend, w_dtype, scale_dtype):
+    """bf16 activations with reference-layout scales (the MFMA decode kernel takes K-blocked ones)."""
+    p = O.make_problem(2, 2048, 1024, w_dtype=w_dtype, x_dtype=O.DT_BFLOAT16, scale_dtype=scale_dtype,
+                       block_axis=1, block_size=256, bias=True, seed=300 + w_dtype)
+    r, y = _run(backend, p)
+    _check(p, y)
+
+
+@pytest.mark.parametrize("act", range(6))
+def test_gemv_activations(backend, act):
+    p = O.make_problem(1, 1024, 1024, w_dtype=O.DT_INT8, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32,
+                       block_axis=1, block_size=32, bias=True, act=act, scale_range=(0.01, 0.05), seed=400 + act)
+    r, y = _run(backend, p)
+    _check(p, y, act_slack=2.0)
+
+
+@pytest.mark.parametrize("shape", [(1, 1100, 1032, 96), (4, 1300, 1032, 1032), (2, 257, 4104, 40),
+                                   (3, 4096, 264, 33 * 8)])
+@pytest.mark.parametrize("w_dtype", [O.DT_INT8, O.DT_INT4])
+def test_gemv_ragged(backend, shape, w_dtype):
+    """K not a multiple of the slice, N not a multiple of the column block, blocks straddling
+    column blocks, a block size >= N (one scale per row)."""
+    M, K, N, B = shape
+    p = O.make_problem(M, K, N, w_dtype=w_dtype, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32, block_axis=1,
+                       block_size=B, bias=True, zp=True, seed=500 + K + w_dtype)
+    r, y = _run(backend, p)
+    _check(p, y)
+
+
+def test_gemv_deterministic_and_exact_option(backend):
+    """Repeated calls give the same bits (split-K partials summed in a fixed order, counters
+    reset); the "exact" option runs the reference-order kernel, bit-identical to the oracle."""
+    p = O.make_problem(1, 4096, 2048, w_dtype=O.DT_INT4, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32,
+                       block_axis=1, block_size=128, bias=True, seed=600)
+    r, y1 = _run(backend, p)
+    assert np.array_equal(y1, r.run())
+    _check(p, y1)
+    ex = ca.New("exact")
+    try:
+        r2 = QDenseRun(ex, p)
+        assert r2.plan() == "qdense_exact"
+        y2 = r2.run()
+    finally:
+        ex.Finalize()
+    assert np.array_equal(y2.view(np.uint32), O.qdense_f32(p).view(np.uint32))
+
+
+@pytest.mark.parametrize("name,M,K,N,G", [("1x64x64_g64", 1, 64, 64, 64), ("8x128x256_g128", 8, 128, 256, 128),
+                                         ("32x512x1024_g128", 32, 512, 1024, 128)])
+@pytest.mark.parametrize("scheme", [O.QUANT_NF4, O.QUANT_LINEAR])
+def test_reference_benchmark_shapes_bit_exact(backend, name, M, K, N, G, scheme):
+    """The reference's BenchmarkQuantizedDense problems (support/backendtest/benchmarks.go:435-470:
+    f32 x, Uint8 NF4 codes or Int8 weights, scales [K, ceil(N/G)] BlockAxis 1, bias): small enough
+    for the reference-order kernel, so bit-identical to the oracle."""
+    w_dtype = O.DT_UINT8 if scheme == O.QUANT_NF4 else O.DT_INT8
+    p = O.make_problem(M, K, N, w_dtype=w_dtype, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32, block_axis=1,
+                       block_size=G, bias=True, scheme=scheme, x_dist="uniform", seed=700 + M)
+    r = QDenseRun(backend, p)
+    assert r.plan() == "qdense_exact"
+    assert np.array_equal(r.run().view(np.uint32), O.qdense_f32(p).view(np.uint32))
