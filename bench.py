@@ -136,7 +136,7 @@ def extra_entry(wl, r):
     nbytes = wl.algorithmic_bytes()
     e = {"us_per_call": round(r["ms_per_step"] * 1e3, 2), "kernel": r["kernel"], "kernel_us": round(r["kernel_us"], 3),
          "kernel_us_per_call": round(r["kernel_us_per_step"], 3)}
-    if wl.name.startswith("C4"):
+    if wl.name.startswith("C4") or wl.name.startswith("D1"):
         e["TFLOPs_kernel"] = round(wl.flops() / (r["kernel_us"] * 1e-6) / 1e12, 1)
         e["roofline"] = mfma_roofline(wl.flops(), r["kernel_us"], traffic_for(wl.name))
     elif wl.name.startswith("C5"):

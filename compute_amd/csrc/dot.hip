@@ -98,6 +98,22 @@ int dot_run(mx_backend* b, const DotDesc& d) {
     MX_CHECK_HIP(hipMemsetAsync(d.out, 0, bytes, b->stream));
     return MX_OK;
   }
+  if (dot_mfma_fits(d))
+    return dot_mfma_run(b, d, d.in_dt == MX_DTYPE_BFLOAT16 ? "dot_mfma_bf16" : "dot_mfma_f16");
+  if (dtype_is_half(d.in_dt) && d.out_dt != MX_DTYPE_FLOAT32) {
+    // Half output folded in by the graph compiler, on a path that sums into f32 memory: the f32
+    // result goes to a temporary, then ConvertDType's own kernel rounds it (the same arithmetic).
+    void* tmp = nullptr;
+    const int64_t n = d.B * d.M * d.N;
+    MX_TRY(dev_alloc(b, (size_t)n * sizeof(float), &tmp));
+    DotDesc d2 = d;
+    d2.out = tmp;
+    d2.out_dt = MX_DTYPE_FLOAT32;
+    int rc = dot_run(b, d2);
+    if (rc == MX_OK) rc = ew_convert(b, tmp, MX_DTYPE_FLOAT32, d.out, d.out_dt, n);
+    dev_free(b, tmp);  // stream-ordered pool: later users run after these kernels
+    return rc;
+  }
   if (d.B > 65535) return set_error(MX_ERR_INVALID, "DotGeneral: batch size %lld too large", (long long)d.B);
   dim3 grid((unsigned)((d.N + kDotTile - 1) / kDotTile), (unsigned)((d.M + kDotTile - 1) / kDotTile), (unsigned)d.B);
   if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "DotGeneral: M too large");

@@ -1152,6 +1152,24 @@ static void fuse_dense_pairs(const FunctionImpl& f, std::vector<Node>& nodes) {
   }
 }
 
+// DotGeneral over half inputs sums into f32, then ConvertDType rounds back (dot.go:340-372): when
+// the f32 sum has no other use, the rounding moves into the contraction's epilogue.
+static void fuse_dot_convert(const FunctionImpl& f, std::vector<Node>& nodes) {
+  std::vector<int> uses = count_uses(f, nodes);
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    Node& n = nodes[i];
+    if (n.op != Op::kConvert || !dtype_is_half(n.shape.dtype)) continue;
+    const int q = n.in[0];
+    const Node& dn = nodes[q];
+    if (dn.op != Op::kDotNorm || dn.shape.dtype != MX_DTYPE_FLOAT32 || uses[q] != 1) continue;
+    if (nodes[dn.in[0]].shape.dtype != n.shape.dtype) continue;
+    Node fused = dn;
+    fused.shape.dtype = n.shape.dtype;
+    n = fused;
+    uses = count_uses(f, nodes);
+  }
+}
+
 // RMS normalisation written out with standard ops (as a GoMLX model builds it):
 //   xf = ConvertDType(x bf16 [M, D] -> f32); ss = ReduceSum(Mul(xf, xf), axis 1);
 //   t = Add(Mul(ss, c), e) with c, e f32 [M]; inv = Rsqrt(t);
@@ -1242,6 +1260,7 @@ int mx_builder_compile(mx_builder* bld, mx_executable** out) {
     fuse_rms_norm(bld->fn, e->nodes);
     fuse_dense_epilogues(bld->fn, e->nodes);
     fuse_dense_pairs(bld->fn, e->nodes);
+    fuse_dot_convert(bld->fn, e->nodes);
   }
   const int nn = (int)e->nodes.size();
 

@@ -269,9 +269,12 @@ struct DotDesc {
   void* out;
   int64_t B, M, K, N;
   bool rhs_transposed;
-  int in_dt, out_dt;  // out_dt: F32 for half inputs, else in_dt (conversion handled by caller)
+  int in_dt, out_dt;  // F32 for half inputs (or the half dtype itself: the rounding folded in), else in_dt
 };
 int dot_run(mx_backend* b, const DotDesc& d);
+// Half-precision DotGeneral on the matrix cores (qdense_gemm.hip).
+bool dot_mfma_fits(const DotDesc& d);
+int dot_mfma_run(mx_backend* b, const DotDesc& d, const char* name);
 
 // Elementwise / data-movement kernels (elementwise.hip).
 int ew_convert(mx_backend* b, const void* in, int in_dt, void* out, int out_dt, int64_t n);

@@ -41,6 +41,7 @@ namespace mx {
 namespace {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
@@ -55,18 +56,30 @@ constexpr int kUnroll = 4;                           // multiple of kPf and of t
 static_assert(kXLoads * kThreads * 16 == kABytes, "x load split");
 static_assert(kBK * kBN == 16 * kThreads, "conversion: 16 weights per thread");
 
+// B operand kinds: the quantized weights [K, N] (int8 / uint8, converted to bf16), or a
+// DotGeneral right-hand side in bf16 / f16, [K, N] (transposed on the way into LDS) or [N, K].
+enum GemmB { kBI8 = 0, kBU8, kBBf16KN, kBF16KN, kBBf16NK, kBF16NK };
+template <int BK> constexpr bool kDotB = BK >= kBBf16KN;
+template <int BK> constexpr bool kF16B = BK == kBF16KN || BK == kBF16NK;
+template <int BK> constexpr bool kNKB = BK == kBBf16NK || BK == kBF16NK;
+
 struct GemmArgs {
-  const uint16_t* x;  // [M, K] bf16
-  const uint8_t* w;   // [K, N] int8 / uint8
-  const void* scale;  // [N]
-  const void* bias;   // [N] or null
-  uint16_t* out;      // [M, N] bf16
-  int M, K, N, s_dt, b_dt, act, tiles_n, grouped;
+  const uint16_t* x;  // [batch][M, K] bf16 (f16 with an f16 B)
+  const uint8_t* w;   // [K, N] int8 / uint8, or [batch][K, N] / [batch][N, K] half
+  const void* scale;  // [N] (quantized)
+  const void* bias;   // [N] or null (quantized)
+  void* out;          // [M, N] bf16 (quantized) or [batch][M, N] f32 / bf16 / f16 (DotGeneral)
+  int M, K, N, s_dt, b_dt, act, tiles_n, grouped, tiles, out_dt;
 };
 
+template <int BK>
 __device__ __forceinline__ f32x4_t mfma(const u32x4_v& a, const u32x4_v& b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
-                                                 0, 0, 0);
+  if constexpr (kF16B<BK>)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
 }
 
 // Workgroup barrier ordering LDS only: waits for this wave's LDS accesses, not for its global
@@ -106,13 +119,21 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
   }
 }
 
-template <int WDT>
+template <int BK>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // Tile order: consecutive work items go to one XCD (workgroups are dispatched round-robin over
-  // the 8); with whole 2 x 16 tile groups, 32 consecutive items form one group.
+  // the 8); with whole 2 x 16 tile groups, 32 consecutive items form one group.  DotGeneral
+  // batches are consecutive runs of items.
   const int total = gridDim.x;
   const int bid = blockIdx.x;
-  const int item = (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
+  int item = (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
+  const int batch = item / a.tiles;
+  item -= batch * a.tiles;
+  if constexpr (kDotB<BK>) {
+    a.x += (size_t)batch * a.M * a.K;
+    a.w += (size_t)batch * a.K * a.N * 2;
+    a.out = (char*)a.out + (size_t)batch * a.M * a.N * (a.out_dt == MX_DTYPE_FLOAT32 ? 4 : 2);
+  }
   int tm, tn;
   if (a.grouped) {
     const int g = item >> 5, q = item & 31, gpr = a.tiles_n >> 4;
@@ -153,35 +174,83 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < kXLoads; ++i) *(u32x4_v*)(&xs[buf][xdst[i]]) = v[i];
   };
-  // w: thread t converts columns 4*cq .. 4*cq + 3 and rows 4*j .. 4*j + 3 of each block; the 32
-  // threads of a j read 128 contiguous bytes of a row.  Columns past N read column 0 (their
-  // outputs are not stored).
+  // B, [K, N] kinds: thread t converts columns 4*cq .. 4*cq + 3 and rows 4*j .. 4*j + 3 of each
+  // block; the 32 threads of a j read one contiguous row segment (128 bytes of int8, 256 of a
+  // half type).  Columns past N read column 0 (their outputs are not stored).
+  // [N, K] kinds: B rows are k-contiguous like x: thread t copies 16-byte chunks q = t + kThreads*i,
+  // column q / 8 (rows past N read row N-1), k-chunk q % 8.
+  constexpr int kEB = kDotB<BK> ? 2 : 1;  // bytes per B element
   const int cq = t & 31, j = t >> 5;
   const int wcol = n0 + 4 * cq + 4 <= a.N ? n0 + 4 * cq : 0;
-  const uint8_t* wsrc = a.w + (size_t)(4 * j) * N + wcol;
+  const uint8_t* wsrc = a.w + ((size_t)(4 * j) * N + wcol) * kEB;
   // Column 4*cq + c lives in Bt row (4*cq + c) ^ (cq & 1), k-chunk j / 2 swizzled by (cq / 2) & 7.
   const uint32_t cv_off = (uint32_t)((((j >> 1) ^ ((cq >> 1) & 7)) << 4) + ((j & 1) << 3));
-  auto load_w = [&](int kb, uint32_t (&dst)[kWLoads]) {
+  constexpr int kNKLoads = kBtBytes / (kThreads * 16);
+  const uint8_t* nksrc[kNKLoads];
+  uint32_t nkdst[kNKLoads];
+  if constexpr (kNKB<BK>) {
+#pragma unroll
+    for (int i = 0; i < kNKLoads; ++i) {
+      const int q = t + kThreads * i;
+      const int r = q >> 3, c = q & 7, p = r ^ ((r >> 2) & 1);
+      nksrc[i] = a.w + ((size_t)min(n0 + r, a.N - 1) * a.K + 8 * c) * 2;
+      nkdst[i] = (uint32_t)(p * (kBK * 2) + ((c ^ ((p >> 3) & 7)) << 4));
+    }
+  }
+  // Register words of one block of B per thread.
+  constexpr int kWWords = kNKB<BK> ? 4 * kNKLoads : (kDotB<BK> ? 2 * kWLoads : kWLoads);
+  auto load_w = [&](int kb, uint32_t (&dst)[kWWords]) {
     kb = min(kb, KB - 1);
+    if constexpr (kNKB<BK>) {
 #pragma unroll
-    for (int e = 0; e < kWLoads; ++e)
-      dst[e] = __builtin_nontemporal_load((const uint32_t*)(wsrc + (size_t)(kb * kBK + e) * N));
-  };
-  // Four bf16 k-values of each of four consecutive columns (Bt rows 128 bytes apart).
-  auto store_w = [&](const uint32_t (&w4)[kWLoads], int buf) {
+      for (int i = 0; i < kNKLoads; ++i) {
+        const u32x4_v v = __builtin_nontemporal_load((const u32x4_v*)(nksrc[i] + (size_t)kb * kBK * 2));
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float f[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if constexpr (WDT == MX_DTYPE_INT8)
-          f[e] = (float)(int8_t)(w4[e] >> (8 * c));
-        else
-          f[e] = (float)(uint8_t)(w4[e] >> (8 * c));
+        for (int e = 0; e < 4; ++e) dst[4 * i + e] = v[e];
       }
-      *(u32x2_v*)(&bt[buf][cv_off + (uint32_t)((4 * cq + (c ^ (cq & 1))) * (kBK * 2))]) =
-          u32x2_v{__builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u),
-                  __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u)};
+    } else if constexpr (kDotB<BK>) {
+#pragma unroll
+      for (int e = 0; e < kWLoads; ++e) {
+        const u32x2_v v = __builtin_nontemporal_load((const u32x2_v*)(wsrc + (size_t)(kb * kBK + e) * N * 2));
+        dst[2 * e] = v[0];
+        dst[2 * e + 1] = v[1];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kWLoads; ++e)
+        dst[e] = __builtin_nontemporal_load((const uint32_t*)(wsrc + (size_t)(kb * kBK + e) * N));
+    }
+  };
+  // Four k-values of each of four consecutive columns (Bt rows 128 bytes apart): int8 converted
+  // exactly to bf16, half values regrouped by column.  [N, K]: the chunks as loaded.
+  auto store_w = [&](const uint32_t (&w4)[kWWords], int buf) {
+    if constexpr (kNKB<BK>) {
+#pragma unroll
+      for (int i = 0; i < kNKLoads; ++i)
+        *(u32x4_v*)(&bt[buf][nkdst[i]]) = u32x4_v{w4[4 * i], w4[4 * i + 1], w4[4 * i + 2], w4[4 * i + 3]};
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        u32x2_v v;
+        if constexpr (kDotB<BK>) {
+          // Row e holds columns 0..3 as dwords [c0 c1][c2 c3]; column c's k-pairs (e, e+1).
+          const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+          v = u32x2_v{__builtin_amdgcn_perm(w4[2 * 1 + (c >> 1)], w4[2 * 0 + (c >> 1)], sel),
+                      __builtin_amdgcn_perm(w4[2 * 3 + (c >> 1)], w4[2 * 2 + (c >> 1)], sel)};
+        } else {
+          float f[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (BK == kBI8)
+              f[e] = (float)(int8_t)(w4[e] >> (8 * c));
+            else
+              f[e] = (float)(uint8_t)(w4[e] >> (8 * c));
+          }
+          v = u32x2_v{__builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u),
+                      __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u)};
+        }
+        *(u32x2_v*)(&bt[buf][cv_off + (uint32_t)((4 * cq + (c ^ (cq & 1))) * (kBK * 2))]) = v;
+      }
     }
   };
 
@@ -210,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[rb][c] = mfma(A[rb], B[c], acc[rb][c]);
+      for (int c = 0; c < 4; ++c) acc[rb][c] = mfma<BK>(A[rb], B[c], acc[rb][c]);
   };
 
   // Register slots hold the next kPf blocks' x and w: block kb's slot is free once block kb
@@ -221,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // barrier that publishes block kb + 1, its step-0 reads are issued before step 1's MFMAs.
   // (sched_barrier keeps the compiler from regrouping the phases.)
   u32x4_v xr[kPf][kXLoads];
-  uint32_t wr4[kPf][kWLoads];
+  uint32_t wr4[kPf][kWWords];
   u32x4_v A0[4], B0[4], A1[4], B1[4];
   auto block = [&](int kb, auto step) {
     constexpr int U = decltype(step)::value;  // kb % kUnroll
@@ -284,9 +353,31 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   for (; kb + kUnroll <= KB; kb += kUnroll) blocks(kb, kUnroll, I0{}, I1{}, I2{}, I3{});
   blocks(kb, KB - kb, I0{}, I1{}, I2{});
 
-  // Epilogue: y = act(acc * s[n] + bias[n]) for this lane's 4 columns.
+  // Epilogue: y = act(acc * s[n] + bias[n]) for this lane's 4 columns (DotGeneral: the f32 sums,
+  // or the sums rounded to the half output dtype as ConvertDType rounds them, 4 columns per store).
   const int ncol = n0 + 64 * wc + 4 * cg;
   if (ncol >= a.N) return;
+  if constexpr (kDotB<BK>) {
+    const int r0 = m0 + 64 * wr + 4 * kq;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = r0 + 16 * rb + r;
+        if (row >= a.M) continue;
+        const size_t o = (size_t)row * N + ncol;
+        if (a.out_dt == MX_DTYPE_FLOAT32) {
+          *(f32x4_t*)((float*)a.out + o) = f32x4_t{acc[rb][0][r], acc[rb][1][r], acc[rb][2][r], acc[rb][3][r]};
+        } else {
+          uint32_t h[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            h[c] = a.out_dt == MX_DTYPE_BFLOAT16 ? f32_to_bf16(acc[rb][c][r]) : f32_to_f16(acc[rb][c][r]);
+          *(u32x2_v*)((uint16_t*)a.out + o) = u32x2_v{h[0] | h[1] << 16, h[2] | h[3] << 16};
+        }
+      }
+    return;
+  } else {
   float sc[4], bi[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -294,13 +385,15 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     bi[c] = a.bias ? load_f(a.bias, ncol + c, a.b_dt) : 0.0f;
   }
   const int row0 = m0 + 64 * wr + 4 * kq;
+  uint16_t* out = (uint16_t*)a.out;
   switch (a.act) {
-    case MX_ACT_GELU: store_tile<MX_ACT_GELU>(acc, sc, bi, a.out, row0, a.M, N, ncol); break;
-    case MX_ACT_RELU: store_tile<MX_ACT_RELU>(acc, sc, bi, a.out, row0, a.M, N, ncol); break;
-    case MX_ACT_SILU: store_tile<MX_ACT_SILU>(acc, sc, bi, a.out, row0, a.M, N, ncol); break;
-    case MX_ACT_HARDSWISH: store_tile<MX_ACT_HARDSWISH>(acc, sc, bi, a.out, row0, a.M, N, ncol); break;
-    case MX_ACT_TANH: store_tile<MX_ACT_TANH>(acc, sc, bi, a.out, row0, a.M, N, ncol); break;
-    default: store_tile<MX_ACT_NONE>(acc, sc, bi, a.out, row0, a.M, N, ncol); break;
+    case MX_ACT_GELU: store_tile<MX_ACT_GELU>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+    case MX_ACT_RELU: store_tile<MX_ACT_RELU>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+    case MX_ACT_SILU: store_tile<MX_ACT_SILU>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+    case MX_ACT_HARDSWISH: store_tile<MX_ACT_HARDSWISH>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+    case MX_ACT_TANH: store_tile<MX_ACT_TANH>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+    default: store_tile<MX_ACT_NONE>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+  }
   }
 }
 
@@ -321,7 +414,7 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.w = (const uint8_t*)d.w;
   ga.scale = d.scale;
   ga.bias = d.bias;
-  ga.out = (uint16_t*)d.out;
+  ga.out = d.out;
   ga.M = (int)d.M;
   ga.K = (int)d.K;
   ga.N = (int)d.N;
@@ -333,13 +426,59 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: output too large for the GEMM path");
   ga.tiles_n = (int)tiles_n;
   ga.grouped = (tiles_m % 2 == 0 && tiles_n % 16 == 0) ? 1 : 0;
+  ga.tiles = (int)(tiles_m * tiles_n);
   const int grid = (int)(tiles_m * tiles_n);
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     if (d.w_dt == MX_DTYPE_INT8)
-      dispatch(qdense_gemm_kernel<MX_DTYPE_INT8>, grid, kThreads, 0, st, ga);
+      dispatch(qdense_gemm_kernel<kBI8>, grid, kThreads, 0, st, ga);
     else
-      dispatch(qdense_gemm_kernel<MX_DTYPE_UINT8>, grid, kThreads, 0, st, ga);
+      dispatch(qdense_gemm_kernel<kBU8>, grid, kThreads, 0, st, ga);
+  });
+}
+
+// DotGeneral on the matrix cores: half-precision inputs, f32 sums (the lowering's accumulator,
+// dot/dot.go:340-372), normalized [batch][M, K] x [batch][K, N] or [batch][N, K], stored as f32
+// or rounded to the input's half dtype (the lowering's ConvertDType back, folded in).  Only the
+// summation order differs from a sequential f32 sum (every half product is exact in f32).
+bool dot_mfma_fits(const DotDesc& d) {
+  auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
+  const bool half = d.in_dt == MX_DTYPE_BFLOAT16 || d.in_dt == MX_DTYPE_FLOAT16;
+  return half && (d.out_dt == MX_DTYPE_FLOAT32 || d.out_dt == d.in_dt) && d.M >= 1 && d.K >= kBK && d.K % kBK == 0 && d.N >= 16 &&
+         d.N % 16 == 0 && d.B * d.M * d.N * d.K >= ((int64_t)1 << 24) && d.M < (1 << 30) && d.K < (1 << 30) &&
+         d.N < (1 << 30) && aligned(d.lhs, 16) && aligned(d.rhs, 16) && aligned(d.out, 16);
+}
+
+int dot_mfma_run(mx_backend* b, const DotDesc& d, const char* name) {
+  GemmArgs ga{};
+  ga.x = (const uint16_t*)d.lhs;
+  ga.w = (const uint8_t*)d.rhs;
+  ga.out = d.out;
+  ga.out_dt = d.out_dt;
+  ga.M = (int)d.M;
+  ga.K = (int)d.K;
+  ga.N = (int)d.N;
+  const int64_t tiles_m = (d.M + kBM - 1) / kBM, tiles_n = (d.N + kBN - 1) / kBN;
+  if (d.B * tiles_m * tiles_n > (int64_t)1 << 30)
+    return set_error(MX_ERR_INVALID, "DotGeneral: output too large for the matrix-core path");
+  ga.tiles_n = (int)tiles_n;
+  ga.grouped = (tiles_m % 2 == 0 && tiles_n % 16 == 0) ? 1 : 0;
+  ga.tiles = (int)(tiles_m * tiles_n);
+  const int grid = (int)(d.B * tiles_m * tiles_n);
+  hipStream_t st = b->stream;
+  const bool f16 = d.in_dt == MX_DTYPE_FLOAT16;
+  return launch(b, name, [&] {
+    if (d.rhs_transposed) {
+      if (f16)
+        dispatch(qdense_gemm_kernel<kBF16NK>, grid, kThreads, 0, st, ga);
+      else
+        dispatch(qdense_gemm_kernel<kBBf16NK>, grid, kThreads, 0, st, ga);
+    } else {
+      if (f16)
+        dispatch(qdense_gemm_kernel<kBF16KN>, grid, kThreads, 0, st, ga);
+      else
+        dispatch(qdense_gemm_kernel<kBBf16KN>, grid, kThreads, 0, st, ga);
+    }
   });
 }
 

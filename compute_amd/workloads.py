@@ -177,6 +177,44 @@ class GGMLWorkload:
         return 2 * self.M * self.K * self.N
 
 
+@dataclass
+class DotWorkload:
+    """DotGeneral at the prefill shape (the contraction FusedQuantizedDense lowers onto, SURVEY
+    a12-a14): x [M, K] . w [K, N] in bf16, f32 accumulation, bf16 output."""
+
+    name: str
+    M: int
+    K: int
+    N: int
+    x: np.ndarray
+    w: np.ndarray
+
+    def shapes(self):
+        return [Shape(BFloat16, self.M, self.K), Shape(BFloat16, self.K, self.N)]
+
+    def host_inputs(self):
+        return [self.x, self.w]
+
+    def compile(self, backend: B.Backend) -> B.Executable:
+        bld = backend.Builder(self.name)
+        f = bld.Main()
+        x, w = (f.Parameter(n, s) for n, s in zip(["x", "w"], self.shapes()))
+        f.Return([f.DotGeneral(x, [1], [], w, [0], [])])
+        return bld.Compile()
+
+    def upload(self, backend: B.Backend):
+        return [backend.BufferFromFlatData(0, d.ravel(), s) for d, s in zip(self.host_inputs(), self.shapes())]
+
+    def weight_bytes(self) -> int:
+        return self.w.nbytes
+
+    def algorithmic_bytes(self) -> int:
+        return self.x.nbytes + self.w.nbytes + self.M * self.N * 2
+
+    def flops(self) -> int:
+        return 2 * self.M * self.K * self.N
+
+
 def ggml_rows(t: int, n: int, k: int, rng) -> np.ndarray:
     """Random GGML rows [n, bytesPerRow]: random codes, block scales (f16) in U(0.001, 0.02)."""
     vpb, bpb = B.ggml_values_per_block(t), B.ggml_bytes_per_block(t)
@@ -237,6 +275,11 @@ def make(name: str, seed: int = 0) -> QDWorkload:
             sc = bf16_from_f32(rs.uniform(0.002, 0.02, (K // G, N)).astype(np.float32))
             ws.append((w, sc, K, N))
         return MLPWorkload("C5_mlp_int4_g128_batch8", M, D, F, G, x, ws)
+    if name == "D1":  # DotGeneral bf16 at the C4 (prefill) shape
+        M, K, N = 2048, 4096, 4096
+        x = bf16_from_f32(rx.standard_normal((M, K)).astype(np.float32))
+        w = bf16_from_f32((rw.standard_normal((K, N)) * 0.02).astype(np.float32))
+        return DotWorkload("D1_dotgeneral_bf16_prefill", M, K, N, x, w)
     if name in ("R1", "R2"):  # the reference's own layout at the C2 shape: f32 x, scale [K, N/128]
         M, K, N, G = 1, 4096, 11008, 128
         nf4 = name == "R2"

@@ -235,3 +235,48 @@ def test_pair_equals_unfused(backend, case):
         nf.Finalize()
     for o in outs[1:]:
         assert np.array_equal(outs[0], o)
+
+
+def _dot_graph(backend, M, K, N, dt, transposed=False, batch=1):
+    bld = backend.Builder("dot_half")
+    f = bld.Main()
+    x = f.Parameter("x", Shape(dt, batch, M, K))
+    w = f.Parameter("w", Shape(dt, batch, N, K) if transposed else Shape(dt, batch, K, N))
+    f.Return([f.DotGeneral(x, [2], [0], w, [2] if transposed else [1], [0])])
+    return bld.Compile()
+
+
+def test_dot_convert_fusion_rules(host):
+    """Half DotGeneral: the f32 sum's ConvertDType back to the input dtype folds into the
+    contraction (dot.go:340-372); an explicit f32 output keeps no conversion at all."""
+    assert _dot_graph(host, 4, 64, 32, BFloat16).Describe() == ["DotGeneral"]
+    nf = ca.New("host_only,nofusion")
+    try:
+        assert _dot_graph(nf, 4, 64, 32, BFloat16).Describe() == ["DotGeneral", "ConvertDType"]
+    finally:
+        nf.Finalize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [BFloat16, ca.Float16])
+@pytest.mark.parametrize("shape", [(256, 512, 512, False, 1), (300, 1024, 272, True, 2), (70, 130, 90, False, 3)])
+def test_dot_half_output_equals_unfused(backend, dt, shape):
+    """Matrix-core epilogue rounding (first two shapes) and the f32-temporary fallback (the last,
+    K % 64 != 0) give the bits of the separate ConvertDType."""
+    M, K, N, transposed, batch = shape
+    rng = np.random.default_rng(M + K)
+    xf = rng.standard_normal((batch, M, K)).astype(np.float32)
+    wf = rng.standard_normal((batch, N, K) if transposed else (batch, K, N)).astype(np.float32)
+    cast = bf16_from_f32 if dt == BFloat16 else (lambda a: a.astype(np.float16))
+    x, w = cast(xf), cast(wf)
+    nf = ca.New("nofusion")
+    try:
+        outs = []
+        for b in (backend, nf):
+            e = _dot_graph(b, M, K, N, dt, transposed, batch)
+            bufs = [b.BufferFromFlatData(0, x.ravel(), Shape(dt, *x.shape)),
+                    b.BufferFromFlatData(0, w.ravel(), Shape(dt, *w.shape))]
+            outs.append(e.Execute(bufs)[0].ToFlatData())
+    finally:
+        nf.Finalize()
+    assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))

@@ -177,3 +177,60 @@ def test_fused_dense_random(backend, act):
     want = O.act(pre.astype(np.float32), act)
     scale = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64) + np.abs(b)
     assert np.all(np.abs(y - want) <= 1e-5 * scale + 1e-6)
+
+
+# ---------------------------------------------------------------------------------------------
+# Half-precision DotGeneral on the matrix cores (qdense_gemm.hip, dot_mfma_*): large enough
+# contractions with K % 64 == 0 and N % 16 == 0 take it; its f32 sums differ from a sequential
+# sum only in order (every half product is exact in f32).
+# ---------------------------------------------------------------------------------------------
+def _half(rng, shape, dt):
+    f = rng.standard_normal(shape).astype(np.float32)
+    if dt == ca.BFloat16:
+        h = O.bf16_round(f)
+        return h, O.bf16_to_f32(h)
+    h = f.astype(np.float16)
+    return h, h.astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", [ca.BFloat16, ca.Float16])
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("shape", [(2, 300, 512, 272), (1, 1024, 1024, 1024), (3, 17, 4096, 256)])
+def test_mfma_dot_f32_accumulation(backend, dt, transposed, shape):
+    """OutputDType f32: the matrix-core sums within 1e-5 of sum|terms| of the f64 value; the
+    kernel that ran is the matrix-core one."""
+    B, M, K, N = shape
+    rng = np.random.default_rng(B * 1000 + M + int(dt) + 3 * transposed)
+    lhs, lv = _half(rng, (B, M, K), dt)
+    rhs, rv = _half(rng, (B, N, K) if transposed else (B, K, N), dt)
+    rc = [2] if transposed else [1]
+    backend.ProfileReset()
+    backend.SetProfiling(True)
+    try:
+        y, odt = run(backend, [(lhs, dt), (rhs, dt)],
+                     lambda f, p: f.DotGeneral(p[0], [2], [0], p[1], rc, [0], ca.DotGeneralConfig(OutputDType=ca.Float32)))
+        prof = backend.Profile()
+    finally:
+        backend.SetProfiling(False)
+    assert odt == ca.Float32
+    assert any(k.startswith("dot_mfma") for k in prof), prof
+    truth = O.dot_general(lv.astype(np.float64), [2], [0], rv.astype(np.float64), rc, [0])
+    scale = O.dot_general(np.abs(lv).astype(np.float64), [2], [0], np.abs(rv).astype(np.float64), rc, [0])
+    assert np.all(np.abs(y.astype(np.float64) - truth) <= 1e-5 * scale)
+
+
+@pytest.mark.parametrize("dt", [ca.BFloat16, ca.Float16])
+def test_mfma_dot_half_output_and_prefill_shape(backend, dt):
+    """The prefill-shaped contraction x [2048, 4096] . W [4096, 4096] in half precision with the
+    lowering's f32 accumulator and half output (rounded once), rel 1e-2 / abs 1e-3 of the f64
+    value, on 256 sampled rows."""
+    rng = np.random.default_rng(11 + int(dt))
+    M, K, N = 2048, 4096, 4096
+    lhs, lv = _half(rng, (M, K), dt)
+    rhs, rv = _half(rng, (K, N), dt)
+    y, odt = run(backend, [(lhs, dt), (rhs, dt)], lambda f, p: f.DotGeneral(p[0], [1], [], p[1], [0], []))
+    assert odt == dt
+    rows = rng.choice(M, 256, replace=False)
+    truth = lv[rows].astype(np.float64) @ rv.astype(np.float64)
+    got = O.bf16_to_f32(y[rows]) if dt == ca.BFloat16 else y[rows].astype(np.float32)
+    assert np.all(np.abs(got - truth) <= 1e-3 + 1e-2 * np.abs(truth))
