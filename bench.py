@@ -9,8 +9,10 @@ weights from HBM rather than the 256 MB Infinity Cache.
 
 The JSON line also reports, under "extra", the other BASELINE configurations measured the same
 way: C3 batched decode (HBM roofline), C4 prefill (bf16 MFMA roofline) and C5, the quantized MLP
-graph built through the Builder API (microseconds per Execute, 100 resident calls); and G1 / G2,
-the GGML block-format decode GEMV (Q4_0 / Q4_K rows, f32 x [1,4096], 11008 rows; HBM roofline).
+graph built through the Builder API (microseconds per Execute, 100 resident calls); G1 / G2,
+the GGML block-format decode GEMV (Q4_0 / Q4_K rows, f32 x [1,4096], 11008 rows; HBM roofline);
+R1, the reference's own layout at the C2 shape (f32 x, Int4, scales [4096, 86]; HBM roofline);
+and D1, bf16 DotGeneral at the C4 shape (bf16 MFMA roofline).
 
 `value` is algorithmic bytes per step / wall time per step over K back-to-back steps (host
 launch overhead included).  `roofline` prices the dominant kernel's average duration, taken from
@@ -157,7 +159,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--extra", default="C3,C4,C5,G1,G2", help="comma list of other configs to report under 'extra'")
+    ap.add_argument("--extra", default="C3,C4,C5,G1,G2,R1,D1", help="comma list of other configs to report under 'extra'")
     ap.add_argument("--only", default="", help="run only this config (profiling passes); prints its entry")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
