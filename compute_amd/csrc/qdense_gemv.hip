@@ -104,7 +104,11 @@ __device__ __forceinline__ void gv_pin(float (&v)[MR]) {
   }
 }
 
-template <int WK, int MR>
+// AX: the scale layout.  1: the reference's [K, ceil(N/B)] (the scale varies along K and is
+// folded into x row by row).  0: blocks of B rows along K, [ceil(K/B), N] (B % 32 == 0 or B >= K,
+// so a wave's 32 rows share one group: the wave sums x*w' and x over its rows and applies its
+// columns' scale and zero point once).
+template <int WK, int MR, int AX>
 __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
   constexpr bool k4 = WK == kGvI4 || WK == kGvU4 || WK == kGvNF4;
   constexpr bool kNF = WK == kGvNF8 || WK == kGvNF4;
@@ -132,7 +136,7 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
   const int nbw = (min(cblk + kCols, a.N) - 1) / a.B - b0 + 1;
   const int jb = min(col0, a.N - 1) / a.B - b0;  // this lane's block (its columns share it)
   constexpr int kXW = kGvRows * MR;                  // floats of staged x per wave
-  constexpr int kSW = kGvRows * kGvSStride;          // floats of staged scales per wave
+  constexpr int kSW = AX ? kGvRows * kGvSStride : 0;  // floats of staged scales per wave
   float* xw = lds + wave * (kXW + 2 * kSW);
   float* sw = xw + kXW;
   float* zw = sw + kSW;
@@ -147,17 +151,25 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) xv[m] = gv_word(a.x, (int64_t)min(m, M - 1) * a.K + k, a.x_dt, a.x);
   }
-  constexpr int kSL = (kGvRows * kGvMaxBlocks + 63) / 64;  // staging loads per lane (upper bound)
+  // AX = 1: the scale/zero-point blocks, staged into LDS.  AX = 0: this lane's columns of its
+  // wave's group, kept in registers.
+  constexpr int kSL = AX ? (kGvRows * kGvMaxBlocks + 63) / 64 : CPL;  // staging loads per lane
   const int nstage = kGvRows * nbw;
   GvWord sv[kSL], zv[kSL];
-  int soff[kSL];  // LDS slot of each staged value (-1: none), computed before the weight loads
+  int soff[kSL];  // AX = 1: LDS slot of each staged value (-1: none), computed before the weight loads
 #pragma unroll
   for (int i = 0; i < kSL; ++i) {
-    const int e = min(lane + 64 * i, nstage - 1);
-    const int r = e / nbw, j = e - r * nbw;
-    const int k = min(kw + r, a.K - 1);
-    const int64_t si = (int64_t)k * a.nblk + b0 + j;
-    soff[i] = lane + 64 * i < nstage ? r * kGvSStride + j : -1;
+    int64_t si;
+    if constexpr (AX) {
+      const int e = min(lane + 64 * i, nstage - 1);
+      const int r = e / nbw, j = e - r * nbw;
+      const int k = min(kw + r, a.K - 1);
+      si = (int64_t)k * a.nblk + b0 + j;
+      soff[i] = lane + 64 * i < nstage ? r * kGvSStride + j : -1;
+    } else {
+      si = (int64_t)(min(kw, a.K - 1) / a.B) * a.N + min(col0 + i, a.N - 1);
+      soff[i] = 0;
+    }
     sv[i] = gv_word(a.scale, si, a.s_dt, a.x);
     zv[i] = gv_word(a.zp, si, a.zp_dt, a.x);
   }
@@ -172,22 +184,26 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
   // Lanes past the row end read its first dword instead (their columns are never stored); rows
   // past K read row K-1 (their x is 0).
   const uint8_t* wp = a.w + (lbyte + 4 <= row_bytes ? lbyte : 0);
+  // Issued in row order (the rows are computed in that order and loads complete in order).
   uint32_t wv[kGvRows];
 #pragma unroll
-  for (int r = 0; r < kGvRows; ++r)
+  for (int r = 0; r < kGvRows; ++r) {
     wv[r] = __builtin_nontemporal_load((const uint32_t*)(wp + (size_t)min(kw + r, a.K - 1) * row_bytes));
-  __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   lut[lane & 15] = lut_v;  // every lane: 4 identical writes per entry
   if (lane < kGvRows) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) xw[lane * MR + m] = kw + lane < a.K ? gv_value(xv[m], a.x_dt) : 0.0f;
   }
+  if constexpr (AX) {
 #pragma unroll
-  for (int i = 0; i < kSL; ++i) {
-    if (soff[i] >= 0) {
-      sw[soff[i]] = gv_value(sv[i], a.s_dt);
-      zw[soff[i]] = has_zp ? gv_value(zv[i], a.zp_dt) : 0.0f;
+    for (int i = 0; i < kSL; ++i) {
+      if (soff[i] >= 0) {
+        sw[soff[i]] = gv_value(sv[i], a.s_dt);
+        zw[soff[i]] = has_zp ? gv_value(zv[i], a.zp_dt) : 0.0f;
+      }
     }
   }
   __syncthreads();
@@ -202,17 +218,20 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
   }
 #pragma unroll
   for (int r = 0; r < kGvRows; ++r) {
-    const float s = sw[r * kGvSStride + jb];
     float xr[MR], xs[MR];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      xr[m] = xw[r * MR + m];
-      xs[m] = xr[m] * s;
-    }
-    {  // branch-free: the staged zero points are 0 without a zero point
+    for (int m = 0; m < MR; ++m) xr[m] = xw[r * MR + m];
+    if constexpr (AX) {
+      const float s = sw[r * kGvSStride + jb];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) xs[m] = xr[m] * s;
+      // branch-free: the staged zero points are 0 without a zero point
       const float z = zw[r * kGvSStride + jb];
 #pragma unroll
       for (int m = 0; m < MR; ++m) zs[m] = __builtin_fmaf(xr[m], z, zs[m]);
+    } else {
+#pragma unroll
+      for (int m = 0; m < MR; ++m) xs[m] = xr[m];
     }
     float wf[CPL];
     const uint32_t v = wv[r] ^ kFlip;
@@ -236,7 +255,7 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      if (kOff != 0.0f) sxs[m] += xs[m];
+      if (kOff != 0.0f || !AX) sxs[m] += xs[m];
 #pragma unroll
       for (int c = 0; c < CPL; ++c) acc[c][m] = __builtin_fmaf(xs[m], wf[c], acc[c][m]);
     }
@@ -251,11 +270,23 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
       asm volatile("" ::: "memory");
     }
   }
+  if constexpr (AX) {
 #pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    const float corr = zs[m] - kOff * sxs[m];
+    for (int m = 0; m < MR; ++m) {
+      const float corr = zs[m] - kOff * sxs[m];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) acc[c][m] += corr;
+      for (int c = 0; c < CPL; ++c) acc[c][m] += corr;
+    }
+  } else {
+    // The group's scale and zero point: (sum x*w' - offset * sum x) * s + zp * sum x.
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const float sc = gv_value(sv[c], a.s_dt);
+      const float zc = has_zp ? gv_value(zv[c], a.zp_dt) : 0.0f;
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        acc[c][m] = __builtin_fmaf(zc, sxs[m], (acc[c][m] - kOff * sxs[m]) * sc);
+    }
   }
 
   // Every wave's tile (rows < M) into LDS as [waves][M][kCols] (over the staging areas, once
@@ -358,7 +389,7 @@ static int gemv_kind(const QDenseDesc& d) {
 static bool gv_float_dt(int dt) { return dt == MX_DTYPE_FLOAT32 || dt == MX_DTYPE_BFLOAT16; }
 
 bool qdense_gemv_fits(const QDenseDesc& d) {
-  if (d.M < 1 || d.M > kGvMaxRows || d.block_axis != 1) return false;
+  if (d.M < 1 || d.M > kGvMaxRows) return false;
   if (d.scheme != MX_QUANT_LINEAR && d.scheme != MX_QUANT_NF4) return false;
   const int kind = gemv_kind(d);
   if (kind < 0 || !gv_float_dt(d.x_dt) || !gv_float_dt(d.s_dt)) return false;
@@ -367,17 +398,27 @@ bool qdense_gemv_fits(const QDenseDesc& d) {
   const bool packed = dtype_is_packed(d.w_dt);
   const int cpl = packed ? 8 : 4;
   auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
+  const bool blocks = d.block_axis == 1 ? d.block_size >= kGvMinBlock && d.block_size % cpl == 0
+                                        : d.block_size % kGvRows == 0 || d.block_size >= d.K;
   return d.K >= 1 && d.K * d.N >= kGvMinWeights && d.K < (int64_t)1 << 30 && d.N < (int64_t)1 << 30 &&
-         d.N % (packed ? 8 : 4) == 0 && d.block_size >= kGvMinBlock && d.block_size % cpl == 0 &&
-         aligned(d.w, 4) && aligned(d.out, d.x_dt == MX_DTYPE_FLOAT32 ? 16 : 8);
+         d.N % (packed ? 8 : 4) == 0 && blocks && aligned(d.w, 4) &&
+         aligned(d.out, d.x_dt == MX_DTYPE_FLOAT32 ? 16 : 8);
+}
+
+template <int WK, int AX>
+static void gemv_launch_ax(const GemvArgs& ga, int grid, size_t lds, hipStream_t st) {
+  if (ga.M == 1)
+    dispatch(qdense_gemv_kernel<WK, 1, AX>, grid, kGvThreads, lds, st, ga);
+  else
+    dispatch(qdense_gemv_kernel<WK, kGvMaxRows, AX>, grid, kGvThreads, lds, st, ga);
 }
 
 template <int WK>
-static void gemv_launch(const GemvArgs& ga, int grid, size_t lds, hipStream_t st) {
-  if (ga.M == 1)
-    dispatch(qdense_gemv_kernel<WK, 1>, grid, kGvThreads, lds, st, ga);
+static void gemv_launch(const GemvArgs& ga, int axis, int grid, size_t lds, hipStream_t st) {
+  if (axis == 1)
+    gemv_launch_ax<WK, 1>(ga, grid, lds, st);
   else
-    dispatch(qdense_gemv_kernel<WK, kGvMaxRows>, grid, kGvThreads, lds, st, ga);
+    gemv_launch_ax<WK, 0>(ga, grid, lds, st);
 }
 
 int qdense_gemv_run(mx_backend* b, const QDenseDesc& d, const char* name) {
@@ -406,7 +447,7 @@ int qdense_gemv_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.M = (int)d.M;
   ga.K = (int)d.K;
   ga.N = (int)d.N;
-  ga.B = (int)std::min<int64_t>(d.block_size, d.N);
+  ga.B = (int)std::min<int64_t>(d.block_size, d.block_axis == 1 ? d.N : d.K);
   ga.S = (int)S;
   ga.nblk = (int)((d.N + d.block_size - 1) / d.block_size);
   ga.act = d.act;
@@ -415,19 +456,20 @@ int qdense_gemv_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.zp_dt = d.zp_dt;
   ga.b_dt = d.b_dt;
   const int mr = d.M == 1 ? 1 : kGvMaxRows;
-  const size_t stage = (size_t)kGvWaves * (kGvRows * mr + 2 * kGvRows * kGvSStride) * sizeof(float);
+  const size_t stage =
+      (size_t)kGvWaves * (kGvRows * mr + (d.block_axis == 1 ? 2 * kGvRows * kGvSStride : 0)) * sizeof(float);
   const size_t tiles = (size_t)kGvWaves * d.M * cols * sizeof(float);
   const size_t lds = std::max(stage, tiles);
   const int grid = (int)(nb * S);
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     switch (gemv_kind(d)) {
-      case kGvI8: gemv_launch<kGvI8>(ga, grid, lds, st); break;
-      case kGvU8: gemv_launch<kGvU8>(ga, grid, lds, st); break;
-      case kGvI4: gemv_launch<kGvI4>(ga, grid, lds, st); break;
-      case kGvU4: gemv_launch<kGvU4>(ga, grid, lds, st); break;
-      case kGvNF8: gemv_launch<kGvNF8>(ga, grid, lds, st); break;
-      default: gemv_launch<kGvNF4>(ga, grid, lds, st); break;
+      case kGvI8: gemv_launch<kGvI8>(ga, d.block_axis, grid, lds, st); break;
+      case kGvU8: gemv_launch<kGvU8>(ga, d.block_axis, grid, lds, st); break;
+      case kGvI4: gemv_launch<kGvI4>(ga, d.block_axis, grid, lds, st); break;
+      case kGvU4: gemv_launch<kGvU4>(ga, d.block_axis, grid, lds, st); break;
+      case kGvNF8: gemv_launch<kGvNF8>(ga, d.block_axis, grid, lds, st); break;
+      default: gemv_launch<kGvNF4>(ga, d.block_axis, grid, lds, st); break;
     }
   });
 }

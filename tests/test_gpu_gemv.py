@@ -126,3 +126,46 @@ def test_reference_benchmark_shapes_bit_exact(backend, name, M, K, N, G, scheme)
     r = QDenseRun(backend, p)
     assert r.plan() == "qdense_exact"
     assert np.array_equal(r.run().view(np.uint32), O.qdense_f32(p).view(np.uint32))
+
+
+# ---------------------------------------------------------------------------------------------
+# K-blocked scales (BlockAxis = 0, [ceil(K/B), N]) at decode: f32 x, zero points and NF4 (the
+# MFMA decode kernel takes bf16 x with plain Linear scales).
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("w_dtype", W_DTYPES)
+@pytest.mark.parametrize("B,zp", [(128, False), (32, True), (None, True)])
+@pytest.mark.parametrize("M", [1, 4])
+def test_gemv_kblocked_f32(backend, w_dtype, B, zp, M):
+    K = 2048
+    p = O.make_problem(M, K, 768, w_dtype=w_dtype, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32, block_axis=0,
+                       block_size=B if B else K, per_channel_1d=B is None, bias=True, zp=zp,
+                       seed=800 + M * 7 + w_dtype + (B or 0))
+    r, y = _run(backend, p)
+    assert r.plan().endswith("_zp") == zp
+    _check(p, y)
+
+
+@pytest.mark.parametrize("w_dtype,scheme,zp", [(O.DT_INT4, O.QUANT_NF4, False), (O.DT_UINT8, O.QUANT_NF4, False),
+                                               (O.DT_INT8, O.QUANT_LINEAR, True), (O.DT_UINT4, O.QUANT_LINEAR, True)])
+def test_gemv_kblocked_bf16_nf4_zp(backend, w_dtype, scheme, zp):
+    p = O.make_problem(2, 4096, 512, w_dtype=w_dtype, x_dtype=O.DT_BFLOAT16, scale_dtype=O.DT_BFLOAT16,
+                       block_axis=0, block_size=64, bias=False, zp=zp, scheme=scheme, seed=900 + w_dtype)
+    r, y = _run(backend, p)
+    _check(p, y)
+
+
+def test_gemv_kblocked_plain_bf16_stays_on_mfma(backend):
+    p = O.make_problem(1, 2048, 1024, w_dtype=O.DT_INT4, x_dtype=O.DT_BFLOAT16, scale_dtype=O.DT_BFLOAT16,
+                       block_axis=0, block_size=128, bias=False, seed=901)
+    assert QDenseRun(backend, p).plan().startswith("qdense_skinny_mfma")
+
+
+@pytest.mark.parametrize("shape", [(3, 1100, 1032, 96), (1, 4000, 264, 4000), (2, 257 * 4, 4104, 64)])
+def test_gemv_kblocked_ragged(backend, shape):
+    """K not a multiple of the slice (a group straddles slices), N not a multiple of the column
+    block, per-channel scales."""
+    M, K, N, B = shape
+    p = O.make_problem(M, K, N, w_dtype=O.DT_INT4, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32, block_axis=0,
+                       block_size=B, bias=True, zp=True, seed=950 + K)
+    r, y = _run(backend, p)
+    _check(p, y)
