@@ -90,10 +90,16 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// act(v * s + b) rounded to bf16, for a compile-time activation.
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+
+// act(v * s + b) for two columns, rounded to a bf16 pair by the hardware conversion
+// (v_cvt_pk_bf16_f32: round to nearest even, the same bits as f32_to_bf16 for every non-NaN
+// value), for a compile-time activation.
 template <int ACT>
-__device__ __forceinline__ uint32_t scaled_act_bf16(float v, float s, float b) {
-  return f32_to_bf16(act_fast(v * s + b, ACT));
+__device__ __forceinline__ uint32_t scaled_act_bf16x2(float v0, float s0, float b0, float v1, float s1, float b1) {
+  const f32x2_t y = {act_fast(v0 * s0 + b0, ACT), act_fast(v1 * s1 + b1, ACT)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2_t));
 }
 
 // Epilogue of one lane: scale, bias, activation, bf16, 8-byte stores of 4 consecutive columns
@@ -111,8 +117,7 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
         uint32_t o[2];
 #pragma unroll
         for (int c = 0; c < 4; c += 2)
-          o[c / 2] = scaled_act_bf16<ACT>(acc[rb][c][r], sc[c], bi[c]) |
-                     (scaled_act_bf16<ACT>(acc[rb][c + 1][r], sc[c + 1], bi[c + 1]) << 16);
+          o[c / 2] = scaled_act_bf16x2<ACT>(acc[rb][c][r], sc[c], bi[c], acc[rb][c + 1][r], sc[c + 1], bi[c + 1]);
         *(uint2*)(out + (size_t)row * N + ncol) = make_uint2(o[0], o[1]);
       }
     }
