@@ -265,3 +265,52 @@ def test_fault_injection_flag_is_host_side(host_backend):
     # The knob is set on the host; the allocation it fails happens only on a device backend.
     host_backend.DebugFailAllocAfter(1)
     host_backend.DebugFailAllocAfter(0)
+
+
+def _plan(backend, M, K, N, *, x_dtype, w_dtype, s_dtype, block_axis, block_size, zp=False, scheme=0, act=0):
+    """Kernel choice for a problem; the pointers are aligned placeholders (planning reads no data)."""
+    a = ca._lib.mx_qdense_args()
+    a.x, a.w, a.scale, a.out = 0x10000, 0x20000, 0x30000, 0x40000
+    if zp:
+        a.zero_point = 0x50000
+        a.zero_point_dtype = s_dtype
+    a.M, a.K, a.N = M, K, N
+    a.x_dtype, a.w_dtype, a.scale_dtype = int(x_dtype), int(w_dtype), int(s_dtype)
+    a.scheme, a.block_axis, a.block_size, a.activation = scheme, block_axis, block_size, act
+    return backend.QDensePlan(a)
+
+
+def test_qdense_plan_selection():
+    """Which kernel each regime takes (host-only planning): the MFMA decode kernel for bf16 x with
+    K-blocked scales, the GEMV for the reference's own layout / f32 x / zero points / NF4 at
+    M <= 4, the MFMA GEMM at prefill, the reference-order kernel for small problems and for
+    everything with the "exact" option."""
+    F32, BF16 = ca.Float32, ca.BFloat16
+    for opts, exact in (("host_only", False), ("host_only,exact", True)):
+        b = ca.New(opts)
+        try:
+            def want(name):
+                return "qdense_exact" if exact else name
+            assert _plan(b, 1, 4096, 11008, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
+                         block_size=128) == want("qdense_skinny_mfma_i4")
+            assert _plan(b, 1, 4096, 11008, x_dtype=F32, w_dtype=ca.Int4, s_dtype=F32, block_axis=1,
+                         block_size=128) == want("qdense_gemv_i4")
+            assert _plan(b, 3, 4096, 11008, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
+                         block_size=64, zp=True) == want("qdense_gemv_i8_zp")
+            assert _plan(b, 1, 4096, 4096, x_dtype=F32, w_dtype=ca.Uint8, s_dtype=F32, block_axis=1,
+                         block_size=128, scheme=1) == want("qdense_gemv_nf4_8bit")
+            assert _plan(b, 2, 4096, 4096, x_dtype=BF16, w_dtype=ca.Uint4, s_dtype=BF16, block_axis=0,
+                         block_size=64, zp=True) == want("qdense_gemv_u4_zp")
+            assert _plan(b, 1, 4096, 4096, x_dtype=F32, w_dtype=ca.Int4, s_dtype=F32, block_axis=0,
+                         block_size=4096) == want("qdense_gemv_i4")
+            assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
+                         block_size=4096) == want("qdense_gemm_mfma_i8")
+            # Small problems, M > 4 with the reference layout, unsupported block sizes: reference order.
+            assert _plan(b, 1, 512, 1024, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
+                         block_size=64) == "qdense_exact"
+            assert _plan(b, 8, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
+                         block_size=64) == "qdense_exact"
+            assert _plan(b, 1, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
+                         block_size=16) == "qdense_exact"
+        finally:
+            b.Finalize()
