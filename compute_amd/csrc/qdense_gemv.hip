@@ -1,7 +1,8 @@
 // Decode GEMV for the reference's own FusedQuantizedDense formats on gfx950: M <= 4 rows of f32
-// (or bf16) activations, weights [K, N] in Int8 / Uint8 / Int4 / Uint4, scheme Linear (with or
-// without a zero point) or NF4, scales in the reference layout (BlockAxis = 1): scale[k, n/B],
-// shape [K, ceil(N/B)].
+// (or bf16) activations per launch (up to 64 rows as one launch per group of 4, the weights
+// re-read), weights [K, N] in Int8 / Uint8 / Int4 / Uint4, scheme Linear (with or without a zero
+// point) or NF4, scales in the reference layout (BlockAxis = 1): scale[k, n/B], shape
+// [K, ceil(N/B)], or blocked along K.
 //
 // Reference semantics: quantizedDenseLinearInt / quantizedDenseNF4
 // (internal/gobackend/fusedops/quantizeddense.go:586-650) then the activation epilogue
@@ -44,7 +45,8 @@ constexpr int kGvWaves = 8;
 constexpr int kGvThreads = 64 * kGvWaves;
 constexpr int kGvRows = 32;                      // K rows per wave
 constexpr int kGvSlice = kGvRows * kGvWaves;     // K rows per workgroup
-constexpr int kGvMaxRows = 4;                    // M
+constexpr int kGvMaxRows = 4;                    // M of one launch
+constexpr int kGvMaxM = 64;  // larger M runs as launches over groups of kGvMaxRows rows (weights re-read)
 constexpr int kGvMinBlock = 32;                  // smallest block size B
 constexpr int kGvMaxBlocks = 512 / kGvMinBlock + 1;  // scale blocks one workgroup touches
 constexpr int kGvSStride = 32;  // LDS row stride of the staged blocks (a power of two >= kGvMaxBlocks)
@@ -389,7 +391,7 @@ static int gemv_kind(const QDenseDesc& d) {
 static bool gv_float_dt(int dt) { return dt == MX_DTYPE_FLOAT32 || dt == MX_DTYPE_BFLOAT16; }
 
 bool qdense_gemv_fits(const QDenseDesc& d) {
-  if (d.M < 1 || d.M > kGvMaxRows) return false;
+  if (d.M < 1 || d.M > kGvMaxM) return false;
   if (d.scheme != MX_QUANT_LINEAR && d.scheme != MX_QUANT_NF4) return false;
   const int kind = gemv_kind(d);
   if (kind < 0 || !gv_float_dt(d.x_dt) || !gv_float_dt(d.s_dt)) return false;
@@ -421,7 +423,23 @@ static void gemv_launch(const GemvArgs& ga, int axis, int grid, size_t lds, hipS
     gemv_launch_ax<WK, 0>(ga, grid, lds, st);
 }
 
+static int gemv_run_rows(mx_backend* b, const QDenseDesc& d, const char* name);
+
 int qdense_gemv_run(mx_backend* b, const QDenseDesc& d, const char* name) {
+  // Groups of kGvMaxRows rows of x and of the output, one launch each (the split-K counters are
+  // back at zero after every launch, and the launches are ordered on the stream).
+  const size_t xe = d.x_dt == MX_DTYPE_FLOAT32 ? 4 : 2;
+  for (int64_t m0 = 0; m0 < d.M; m0 += kGvMaxRows) {
+    QDenseDesc g = d;
+    g.M = std::min<int64_t>(kGvMaxRows, d.M - m0);
+    g.x = (const char*)d.x + (size_t)m0 * d.K * xe;
+    g.out = (char*)d.out + (size_t)m0 * d.N * xe;
+    MX_TRY(gemv_run_rows(b, g, name));
+  }
+  return MX_OK;
+}
+
+static int gemv_run_rows(mx_backend* b, const QDenseDesc& d, const char* name) {
   const bool packed = dtype_is_packed(d.w_dt);
   const int64_t cols = packed ? 512 : 256;
   const int64_t nb = (d.N + cols - 1) / cols;

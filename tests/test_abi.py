@@ -305,10 +305,12 @@ def test_qdense_plan_selection():
                          block_size=4096) == want("qdense_gemv_i4")
             assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
                          block_size=4096) == want("qdense_gemm_mfma_i8")
-            # Small problems, M > 4 with the reference layout, unsupported block sizes: reference order.
+            # Small problems, M > 64 with the reference layout, unsupported block sizes: reference order.
             assert _plan(b, 1, 512, 1024, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=64) == "qdense_exact"
             assert _plan(b, 8, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
+                         block_size=64) == want("qdense_gemv_i8")
+            assert _plan(b, 65, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=64) == "qdense_exact"
             assert _plan(b, 1, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=16) == "qdense_exact"

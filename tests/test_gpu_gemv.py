@@ -3,7 +3,7 @@
 The reference's FusedQuantizedDense takes f32 x and scales in its own layout, scale[k, n/B]
 (BlockAxis = 1, quantizeddense.go:111-123), with Linear (optionally with a zero point) or NF4
 dequantisation.  Small problems keep the reference-order kernel (bit-identical); at decode sizes
-(K*N >= 2^20, M <= 4) the GEMV kernel runs, whose results differ from the reference loop only by
+(K*N >= 2^20, M <= 64, four rows per launch) the GEMV kernel runs, whose results differ from the reference loop only by
 summation order and the folding of the scale into x:
   - f32 outputs: within 1e-5 of sum|terms| of the f64 value (the north star's fp32 bar);
   - bf16 outputs: within rel 1e-2 / abs 1e-3 of the oracle's f32 result, and the same
@@ -167,5 +167,15 @@ def test_gemv_kblocked_ragged(backend, shape):
     M, K, N, B = shape
     p = O.make_problem(M, K, N, w_dtype=O.DT_INT4, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32, block_axis=0,
                        block_size=B, bias=True, zp=True, seed=950 + K)
+    r, y = _run(backend, p)
+    _check(p, y)
+
+
+@pytest.mark.parametrize("M", [5, 8, 13, 16])
+@pytest.mark.parametrize("w_dtype,scheme,zp", [(O.DT_INT4, O.QUANT_LINEAR, True), (O.DT_UINT8, O.QUANT_NF4, False)])
+def test_gemv_row_groups(backend, M, w_dtype, scheme, zp):
+    """M > 4: one launch per group of four rows (x and output offsets per group)."""
+    p = O.make_problem(M, 1024, 1536, w_dtype=w_dtype, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32,
+                       block_axis=1, block_size=128, bias=True, zp=zp, scheme=scheme, seed=990 + M)
     r, y = _run(backend, p)
     _check(p, y)
