@@ -154,6 +154,24 @@ def extra_entry(wl, r):
     return e
 
 
+def dot_table(ca):
+    """The reference's BenchmarkDotGeneral model shapes (support/backendtest/bench_dotgeneral.go,
+    float32 there) on this backend, in float32 and bfloat16: microseconds per Execute (wall, launch
+    included), the kernels that ran and their time per call."""
+    from compute_amd import workloads
+    backend = ca.New("")
+    for case in workloads.DOT_MODEL_CASES:
+        for dt in (ca.Float32, ca.BFloat16):
+            wl = workloads.DotCaseWorkload(case, dt)
+            r = measure(backend, wl, 50, 5, rotate_bytes=0)
+            e = {"case": case[0], "dtype": dt.name, "us_per_call": round(r["ms_per_step"] * 1e3, 2),
+                 "kernel_us_per_call": round(r["kernel_us_per_step"], 2),
+                 "GFLOPs_call": round(wl.flops() / (r["ms_per_step"] * 1e-3) / 1e9, 1),
+                 "kernels": {k: round(v["avg_us"], 2) for k, v in r["kernels"].items()}}
+            print(json.dumps(e), flush=True)
+    backend.Finalize()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -163,6 +181,8 @@ def main():
     ap.add_argument("--only", default="", help="run only this config (profiling passes); prints its entry")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--dot-table", action="store_true",
+                    help="only time the reference's BenchmarkDotGeneral model shapes (f32 and bf16), one line each")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -175,6 +195,9 @@ def main():
         return
 
     import compute_amd as ca
+    if args.dot_table:
+        dot_table(ca)
+        return
     from compute_amd import workloads
 
     backend = ca.New("mi355x")

@@ -215,6 +215,83 @@ class DotWorkload:
         return 2 * self.M * self.K * self.N
 
 
+# DotGeneral model shapes of the reference's BenchmarkDotGeneral
+# (support/backendtest/bench_dotgeneral.go:20-482): the all-MiniLM-L6-v2 cases and the first
+# bge-small-en-v1.5 batch configurations, as (name, lhs dims, rhs dims, lhs contracting,
+# lhs batch, rhs contracting, rhs batch).  The reference runs them in float32.
+DOT_MODEL_CASES = [
+    ("MiniLM/32x12x13x13.32x12x13x32", (32, 12, 13, 13), (32, 12, 13, 32), [3], [0, 1], [2], [0, 1]),
+    ("MiniLM/32x12x13x32.32x12x32x13", (32, 12, 13, 32), (32, 12, 32, 13), [3], [0, 1], [2], [0, 1]),
+    ("MiniLM/32x13x1536.1536x384", (32, 13, 1536), (1536, 384), [2], [], [0], []),
+    ("MiniLM/32x13x1536.384x1536(T)", (32, 13, 1536), (384, 1536), [2], [], [1], []),
+    ("MiniLM/32x13x384.384x1152", (32, 13, 384), (384, 1152), [2], [], [0], []),
+    ("MiniLM/32x13x384.384x1536", (32, 13, 384), (384, 1536), [2], [], [0], []),
+    ("MiniLM/32x13x384.384x384", (32, 13, 384), (384, 384), [2], [], [0], []),
+    ("MiniLM/416x384.384x1152", (416, 384), (384, 1152), [1], [], [0], []),
+    ("bge/10x192x12x192.10x192x12x32", (10, 192, 12, 192), (10, 192, 12, 32), [3], [0, 2], [1], [0, 2]),
+    ("bge/10x192x1536.384x1536(T)", (10, 192, 1536), (384, 1536), [2], [], [1], []),
+    ("bge/10x192x384.1536x384(T)", (10, 192, 384), (1536, 384), [2], [], [1], []),
+    ("bge/10x192x384.384x384(T)", (10, 192, 384), (384, 384), [2], [], [1], []),
+    ("bge/16x128x12x128.16x128x12x32", (16, 128, 12, 128), (16, 128, 12, 32), [3], [0, 2], [1], [0, 2]),
+    ("bge/16x128x12x32.16x128x12x32", (16, 128, 12, 32), (16, 128, 12, 32), [3], [0, 2], [3], [0, 2]),
+    ("bge/16x128x1536.384x1536(T)", (16, 128, 1536), (384, 1536), [2], [], [1], []),
+    ("bge/16x128x384.1536x384(T)", (16, 128, 384), (1536, 384), [2], [], [1], []),
+    ("bge/16x128x384.384x384(T)", (16, 128, 384), (384, 384), [2], [], [1], []),
+    ("bge/256x8x1536.384x1536(T)", (256, 8, 1536), (384, 1536), [2], [], [1], []),
+    ("bge/256x8x384.1536x384(T)", (256, 8, 384), (1536, 384), [2], [], [1], []),
+    ("bge/256x8x384.384x384(T)", (256, 8, 384), (384, 384), [2], [], [1], []),
+]
+
+
+def dot_case_flops(case) -> int:
+    """2 x (product of the output dims) x (product of the contracting dims)."""
+    _, ls, rs, lc, lb, rc, rb = case
+    out = int(np.prod([ls[a] for a in lb])) * int(np.prod([d for a, d in enumerate(ls) if a not in lc + lb])) * \
+        int(np.prod([d for a, d in enumerate(rs) if a not in rc + rb]))
+    return 2 * out * int(np.prod([ls[a] for a in lc]))
+
+
+@dataclass
+class DotCaseWorkload:
+    """One DOT_MODEL_CASES entry in a float dtype: DotGeneral(lhs, rhs) with seeded N(0,1) data."""
+
+    case: tuple
+    dtype: DType
+    seed: int = 0
+
+    @property
+    def name(self) -> str:
+        return f"{self.case[0]}[{self.dtype.name}]"
+
+    def shapes(self):
+        return [Shape(self.dtype, *self.case[1]), Shape(self.dtype, *self.case[2])]
+
+    def host_inputs(self):
+        rng = np.random.default_rng(self.seed)
+        out = []
+        for dims in (self.case[1], self.case[2]):
+            f = rng.standard_normal(dims).astype(np.float32)
+            out.append(bf16_from_f32(f) if self.dtype == BFloat16 else f)
+        return out
+
+    def compile(self, backend: B.Backend) -> B.Executable:
+        _, _, _, lc, lb, rc, rb = self.case
+        bld = backend.Builder("dot_case")
+        f = bld.Main()
+        lhs, rhs = (f.Parameter(n, s) for n, s in zip(["lhs", "rhs"], self.shapes()))
+        f.Return([f.DotGeneral(lhs, lc, lb, rhs, rc, rb)])
+        return bld.Compile()
+
+    def upload(self, backend: B.Backend):
+        return [backend.BufferFromFlatData(0, d.ravel(), s) for d, s in zip(self.host_inputs(), self.shapes())]
+
+    def weight_bytes(self) -> int:
+        return sum(a.nbytes for a in self.host_inputs())
+
+    def flops(self) -> int:
+        return dot_case_flops(self.case)
+
+
 def ggml_rows(t: int, n: int, k: int, rng) -> np.ndarray:
     """Random GGML rows [n, bytesPerRow]: random codes, block scales (f16) in U(0.001, 0.02)."""
     vpb, bpb = B.ggml_values_per_block(t), B.ggml_bytes_per_block(t)
