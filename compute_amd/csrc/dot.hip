@@ -4,8 +4,9 @@
 // [B,N,K] "Transposed" layouts, half-precision inputs accumulating into f32).
 //
 // The tiled kernel stages 64x64 output tiles through LDS, 16-deep in K, each thread owning a
-// 4x4 register block; it serves f32 and f64 (accumulating in the input type) and bf16/f16
-// (accumulating in f32).
+// 4x4 register block; it serves f64, small or unaligned f32 (accumulating in the input type)
+// and small bf16/f16 (accumulating in f32).  Larger f32 contractions run on the matrix cores
+// (dot_f32_mfma_kernel below), larger half ones on qdense_gemm.hip's kernel.
 
 #include "device_common.h"
 #include "mxrt_internal.h"
@@ -90,6 +91,178 @@ __global__ __launch_bounds__(256) void dot_tiled_kernel(const TI* __restrict__ l
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// f32 DotGeneral on the matrix cores: v_mfma_f32_16x16x4_f32 (fp32 products, fp32 sums), so the
+// result differs from a sequential f32 sum only in summation order.  Its dense peak is twice
+// what the VALU reaches without packed fp32.
+//
+// A workgroup (4 waves) owns a (16*TM*WM) x (16*TN*WN) output tile; WM x WN waves split the
+// tile and the remaining KS = 4 / (WM*WN) waves split K (wave w takes K steps w, w+KS, ...),
+// summed through LDS in wave order at the end (deterministic).  Operands come straight from
+// global memory into registers, one step ahead: a wave's K step is 32 deep, lane group g
+// (lane / 16) holding k = 8g .. 8g+7 of row (lane % 16) of each 16-row A tile (two 16-byte
+// loads) and the same k of column (lane % 16) of each 16-column B tile, so MFMA t contracts
+// k = {8g + t}; every lane group reads a 128-byte run of its row.  Rows, columns and k beyond
+// the problem load clamped (in-bounds) addresses and are zeroed by a select; K % 4 == 0.
+// ---------------------------------------------------------------------------------------------
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kF32Step = 32;
+
+// Raw operands of one K step (clamped, in-bounds addresses); dot_f32_mask zeroes what lies
+// beyond the problem when the step is used, so the loads are not waited on where they issue.
+template <bool BT, int TM, int TN>
+__device__ __forceinline__ void dot_f32_load(const float* const (&ap)[TM], const float* const (&bp)[TN], int kb, int g,
+                                             int K, int N, float (&a)[TM][8], float (&bv)[TN][8]) {
+  const int k0 = kb + 8 * g;
+  const int c0 = min(k0, K - 4), c1 = min(k0 + 4, K - 4);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const f32x4_t lo = *(const f32x4_t*)(ap[i] + c0), hi = *(const f32x4_t*)(ap[i] + c1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[i][e] = lo[e];
+      a[i][4 + e] = hi[e];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    if constexpr (BT) {
+      const f32x4_t lo = *(const f32x4_t*)(bp[j] + c0), hi = *(const f32x4_t*)(bp[j] + c1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bv[j][e] = lo[e];
+        bv[j][4 + e] = hi[e];
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) bv[j][t] = bp[j][(int64_t)min(k0 + t, K - 1) * N];
+    }
+  }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void dot_f32_mask(int kb, int g, int K, const float (&ra)[TM][8], const float (&rb)[TN][8],
+                                             float (&a)[TM][8], float (&bv)[TN][8]) {
+  const int k0 = kb + 8 * g;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const bool v = k0 + t < K;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i][t] = v ? ra[i][t] : 0.f;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bv[j][t] = v ? rb[j][t] : 0.f;
+  }
+}
+
+template <bool BT, int WM, int WN, int TM, int TN>
+__global__ __launch_bounds__(256) void dot_f32_mfma_kernel(const float* __restrict__ lhs, const float* __restrict__ rhs,
+                                                           float* __restrict__ out, int M, int K, int N) {
+  constexpr int KS = 4 / (WM * WN);
+  static_assert(KS * WM * WN == 4, "4 waves");
+  __shared__ f32x4_t red[KS > 1 ? (KS - 1) * WM * WN * TM * TN * 64 : 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wk = wave % KS, wmn = wave / KS, wm = wmn / WN, wn = wmn % WN;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t bz = blockIdx.z;
+  const int m0 = blockIdx.y * (16 * TM * WM) + wm * 16 * TM;
+  const int n0 = blockIdx.x * (16 * TN * WN) + wn * 16 * TN;
+  const float* L = lhs + bz * M * K;
+  const float* R = rhs + bz * K * N;
+  const float* ap[TM];
+  const float* bp[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) ap[i] = L + (int64_t)min(m0 + 16 * i + r, M - 1) * K;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = min(n0 + 16 * j + r, N - 1);
+    bp[j] = BT ? R + (int64_t)n * K : R + n;
+  }
+  f32x4_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int steps = (K + kF32Step - 1) / kF32Step;
+  float ra[TM][8], rb[TN][8];
+  dot_f32_load<BT, TM, TN>(ap, bp, wk * kF32Step, g, K, N, ra, rb);
+  for (int s = wk; s < steps; s += KS) {
+    float a[TM][8], bv[TN][8];
+    dot_f32_mask<TM, TN>(s * kF32Step, g, K, ra, rb, a, bv);
+    // Next step's operands (the last step reloads itself: in bounds, unused), issued ahead of
+    // this step's products.
+    dot_f32_load<BT, TM, TN>(ap, bp, min(s + KS, steps - 1) * kF32Step, g, K, N, ra, rb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][t], bv[j][t], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (KS > 1) {
+    if (wk > 0) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) red[(((wk - 1) * WM * WN + wmn) * TM * TN + i * TN + j) * 64 + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int w = 1; w < KS; ++w)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] += red[(((w - 1) * WM * WN + wmn) * TM * TN + i * TN + j) * 64 + lane];
+  }
+  float* O = out + bz * M * N;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + 16 * j + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 16 * i + 4 * g + e;
+        if (m < M && n < N) O[(int64_t)m * N + n] = acc[i][j][e];
+      }
+    }
+}
+
+// Large enough f32 contractions (>= 2^20 multiply-adds) with K % 4 == 0 and 16-byte aligned
+// operands take the matrix cores; small ones keep the tiled kernel's sequential sums.
+static bool dot_f32_mfma_fits(const DotDesc& d) {
+  auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
+  return d.in_dt == MX_DTYPE_FLOAT32 && d.out_dt == MX_DTYPE_FLOAT32 && d.K >= 4 && d.K % 4 == 0 &&
+         d.B * d.M * d.N * d.K >= ((int64_t)1 << 20) && d.B <= 65535 && d.M < (1 << 24) && d.N < (1 << 24) &&
+         d.K < (1 << 24) && aligned(d.lhs, 16) && aligned(d.rhs, 16);
+}
+
+template <bool BT, int WM, int WN, int TM, int TN>
+static int dot_f32_mfma_launch(mx_backend* b, const DotDesc& d) {
+  constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
+  const dim3 grid((unsigned)((d.N + BN - 1) / BN), (unsigned)((d.M + BM - 1) / BM), (unsigned)d.B);
+  if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "DotGeneral: M too large");
+  hipStream_t st = b->stream;
+  return launch(b, "dot_mfma_f32", [&] {
+    dispatch(dot_f32_mfma_kernel<BT, WM, WN, TM, TN>, grid, 256, 0, st, (const float*)d.lhs, (const float*)d.rhs,
+             (float*)d.out, (int)d.M, (int)d.K, (int)d.N);
+  });
+}
+
+// Tile choice: the largest workgroup tile that still gives >= 512 workgroups; K-split waves
+// only when each has several K steps.
+template <bool BT>
+static int dot_f32_mfma_run(mx_backend* b, const DotDesc& d) {
+  auto wgs = [&](int bm, int bn) { return d.B * ((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn); };
+  const int64_t steps = (d.K + kF32Step - 1) / kF32Step;
+  if (wgs(64, 64) >= 512) return dot_f32_mfma_launch<BT, 2, 2, 2, 2>(b, d);
+  if (steps < 8) return dot_f32_mfma_launch<BT, 2, 2, 1, 1>(b, d);
+  if (wgs(32, 32) >= 512) return dot_f32_mfma_launch<BT, 1, 1, 2, 2>(b, d);
+  return dot_f32_mfma_launch<BT, 1, 1, 1, 2>(b, d);
+}
+
 int dot_run(mx_backend* b, const DotDesc& d) {
   MX_TRY(check_device(b));
   if (d.B == 0 || d.M == 0 || d.N == 0) return MX_OK;
@@ -100,6 +273,8 @@ int dot_run(mx_backend* b, const DotDesc& d) {
   }
   if (dot_mfma_fits(d))
     return dot_mfma_run(b, d, d.in_dt == MX_DTYPE_BFLOAT16 ? "dot_mfma_bf16" : "dot_mfma_f16");
+  if (dot_f32_mfma_fits(d))
+    return d.rhs_transposed ? dot_f32_mfma_run<true>(b, d) : dot_f32_mfma_run<false>(b, d);
   if (dtype_is_half(d.in_dt) && d.out_dt != MX_DTYPE_FLOAT32) {
     // Half output folded in by the graph compiler, on a path that sums into f32 memory: the f32
     // result goes to a temporary, then ConvertDType's own kernel rounds it (the same arithmetic).

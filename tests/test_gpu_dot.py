@@ -234,3 +234,57 @@ def test_mfma_dot_half_output_and_prefill_shape(backend, dt):
     truth = lv[rows].astype(np.float64) @ rv.astype(np.float64)
     got = O.bf16_to_f32(y[rows]) if dt == ca.BFloat16 else y[rows].astype(np.float32)
     assert np.all(np.abs(got - truth) <= 1e-3 + 1e-2 * np.abs(truth))
+
+
+# ---------------------------------------------------------------------------------------------
+# f32 DotGeneral on the matrix cores (dot.hip, dot_mfma_f32: v_mfma_f32_16x16x4_f32, fp32
+# products and sums): contractions of >= 2^20 multiply-adds with K % 4 == 0.  The shapes reach
+# every tile configuration (64x64, 32x32 with K split over the waves, 16x32, 32x32 for short K),
+# ragged M and N, K tails inside a 32-deep step, M below one 16-row tile, and the reference's
+# MiniLM projection shape [32*13, 1536] x [1536, 384] (bench_dotgeneral.go).
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("shape", [(1, 416, 1536, 384), (2, 300, 1000, 272), (1, 1024, 1024, 1024),
+                                   (2, 130, 64, 70), (1, 2048, 512, 1024), (192, 128, 32, 128), (1, 5, 4096, 520),
+                                   (3, 777, 36, 1030)])
+def test_mfma_dot_f32(backend, transposed, shape):
+    """Within 1e-5 of sum|terms| of the f64 value (only the summation order differs from a
+    sequential f32 sum), and the kernel that ran is the matrix-core one."""
+    B, M, K, N = shape
+    rng = np.random.default_rng(B * 7919 + M * 31 + K + 5 * transposed)
+    lhs = rng.standard_normal((B, M, K)).astype(np.float32)
+    rhs = rng.standard_normal((B, N, K) if transposed else (B, K, N)).astype(np.float32)
+    rc = [2] if transposed else [1]
+    backend.ProfileReset()
+    backend.SetProfiling(True)
+    try:
+        y, odt = run(backend, [(lhs, ca.Float32), (rhs, ca.Float32)],
+                     lambda f, p: f.DotGeneral(p[0], [2], [0], p[1], rc, [0]))
+        prof = backend.Profile()
+    finally:
+        backend.SetProfiling(False)
+    assert odt == ca.Float32 and y.shape == (B, M, N)
+    assert "dot_mfma_f32" in prof, prof
+    truth = O.dot_general(lhs.astype(np.float64), [2], [0], rhs.astype(np.float64), rc, [0])
+    scale = O.dot_general(np.abs(lhs).astype(np.float64), [2], [0], np.abs(rhs).astype(np.float64), rc, [0])
+    assert np.all(np.abs(y.astype(np.float64) - truth) <= 1e-5 * scale)
+
+
+def test_mfma_dot_f32_special_values_and_repeat(backend):
+    """Inf in a row of lhs reaches only that row's outputs (the zero padding of K tails and
+    clamped columns never multiplies it), and repeated calls give the same bits."""
+    rng = np.random.default_rng(4242)
+    M, K, N = 300, 1028, 200
+    lhs = rng.standard_normal((M, K)).astype(np.float32)
+    rhs = np.abs(rng.standard_normal((K, N))).astype(np.float32)
+    lhs[7, K - 1] = np.inf
+    f = lambda f, p: f.DotGeneral(p[0], [1], [], p[1], [0], [])
+    y1, _ = run(backend, [(lhs, ca.Float32), (rhs, ca.Float32)], f)
+    y2, _ = run(backend, [(lhs, ca.Float32), (rhs, ca.Float32)], f)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    assert np.all(np.isposinf(y1[7]))
+    others = np.delete(np.arange(M), 7)
+    assert np.all(np.isfinite(y1[others]))
+    truth = lhs[others].astype(np.float64) @ rhs.astype(np.float64)
+    scale = np.abs(lhs[others]).astype(np.float64) @ rhs.astype(np.float64)
+    assert np.all(np.abs(y1[others] - truth) <= 1e-5 * scale)
