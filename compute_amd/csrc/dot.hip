@@ -5,8 +5,9 @@
 //
 // The tiled kernel stages 64x64 output tiles through LDS, 16-deep in K, each thread owning a
 // 4x4 register block; it serves f64, small or unaligned f32 (accumulating in the input type)
-// and small bf16/f16 (accumulating in f32).  Larger f32 contractions run on the matrix cores
-// (dot_f32_mfma_kernel below), larger half ones on qdense_gemm.hip's kernel.
+// and small bf16/f16 (accumulating in f32).  Larger contractions run on the matrix cores: the
+// small-tile dot_mm_kernel below (f32, and half problems too small for qdense_gemm.hip's
+// 256x128-tile kernel), or that kernel.
 
 #include "device_common.h"
 #include "mxrt_internal.h"
@@ -92,72 +93,122 @@ __global__ __launch_bounds__(256) void dot_tiled_kernel(const TI* __restrict__ l
 }
 
 // ---------------------------------------------------------------------------------------------
-// f32 DotGeneral on the matrix cores: v_mfma_f32_16x16x4_f32 (fp32 products, fp32 sums), so the
-// result differs from a sequential f32 sum only in summation order.  Its dense peak is twice
-// what the VALU reaches without packed fp32.
+// Small-tile DotGeneral on the matrix cores, for f32 inputs (v_mfma_f32_16x16x4_f32: fp32
+// products and sums, twice the dense rate the VALU reaches without packed fp32) and for half
+// inputs whose problem is too small to fill the chip with qdense_gemm.hip's 256x128 tiles
+// (v_mfma_f32_16x16x32_bf16 / _f16: exact products, f32 sums).  Either way the result differs
+// from a sequential f32 sum only in summation order.
 //
 // A workgroup (4 waves) owns a (16*TM*WM) x (16*TN*WN) output tile; WM x WN waves split the
 // tile and the remaining KS = 4 / (WM*WN) waves split K (wave w takes K steps w, w+KS, ...),
 // summed through LDS in wave order at the end (deterministic).  Operands come straight from
 // global memory into registers, one step ahead: a wave's K step is 32 deep, lane group g
-// (lane / 16) holding k = 8g .. 8g+7 of row (lane % 16) of each 16-row A tile (two 16-byte
-// loads) and the same k of column (lane % 16) of each 16-column B tile, so MFMA t contracts
-// k = {8g + t}; every lane group reads a 128-byte run of its row.  Rows, columns and k beyond
-// the problem load clamped (in-bounds) addresses and are zeroed by a select; K % 4 == 0.
+// (lane / 16) holding k = 8g .. 8g+7 of row (lane % 16) of each 16-row A tile and the same k
+// of column (lane % 16) of each 16-column B tile.  In f32 MFMA t contracts k = {8g + t}; in
+// half one MFMA contracts all 32 (its lane layout is exactly this one).  Every lane group
+// reads a contiguous run of its row.  Rows, columns and k beyond the problem load clamped
+// (in-bounds) addresses and are zeroed by a select when the step is used, so the loads are
+// not waited on where they issue.  f32 needs K % 4 == 0, half K % 8 == 0.
 // ---------------------------------------------------------------------------------------------
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-constexpr int kF32Step = 32;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_v;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_v;
+constexpr int kMmStep = 32;
+enum DotKind { kDkF32 = 0, kDkBf16 = 1, kDkF16 = 2 };
 
-// Raw operands of one K step (clamped, in-bounds addresses); dot_f32_mask zeroes what lies
-// beyond the problem when the step is used, so the loads are not waited on where they issue.
-template <bool BT, int TM, int TN>
-__device__ __forceinline__ void dot_f32_load(const float* const (&ap)[TM], const float* const (&bp)[TN], int kb, int g,
-                                             int K, int N, float (&a)[TM][8], float (&bv)[TN][8]) {
+// Raw operands of one K step: 8 f32 or 8 halves (4 words) per tile per lane.
+template <int KIND, bool BT, int TM, int TN>
+__device__ __forceinline__ void dot_mm_load(const void* const (&ap)[TM], const void* const (&bp)[TN], int kb, int g,
+                                            int K, int N, uint32_t (&ra)[TM][8], uint32_t (&rb)[TN][8]) {
   const int k0 = kb + 8 * g;
-  const int c0 = min(k0, K - 4), c1 = min(k0 + 4, K - 4);
+  if constexpr (KIND == kDkF32) {
+    const int c0 = min(k0, K - 4), c1 = min(k0 + 4, K - 4);
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const f32x4_t lo = *(const f32x4_t*)(ap[i] + c0), hi = *(const f32x4_t*)(ap[i] + c1);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      a[i][e] = lo[e];
-      a[i][4 + e] = hi[e];
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    if constexpr (BT) {
-      const f32x4_t lo = *(const f32x4_t*)(bp[j] + c0), hi = *(const f32x4_t*)(bp[j] + c1);
+    for (int i = 0; i < TM; ++i) {
+      const u32x4_t lo = *((const u32x4_t*)((const float*)ap[i] + c0)), hi = *((const u32x4_t*)((const float*)ap[i] + c1));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        bv[j][e] = lo[e];
-        bv[j][4 + e] = hi[e];
+        ra[i][e] = lo[e];
+        ra[i][4 + e] = hi[e];
       }
-    } else {
+    }
 #pragma unroll
-      for (int t = 0; t < 8; ++t) bv[j][t] = bp[j][(int64_t)min(k0 + t, K - 1) * N];
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (BT) {
+        const u32x4_t lo = *((const u32x4_t*)((const float*)bp[j] + c0)), hi = *((const u32x4_t*)((const float*)bp[j] + c1));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          rb[j][e] = lo[e];
+          rb[j][4 + e] = hi[e];
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) rb[j][t] = ((const uint32_t*)bp[j])[(int64_t)min(k0 + t, K - 1) * N];
+      }
+    }
+  } else {
+    const int c0 = min(k0, K - 8);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const u32x4_t v = *((const u32x4_t*)((const uint16_t*)ap[i] + c0));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ra[i][e] = v[e];
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (BT) {
+        const u32x4_t v = *((const u32x4_t*)((const uint16_t*)bp[j] + c0));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rb[j][e] = v[e];
+      } else {
+        const uint16_t* q = (const uint16_t*)bp[j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          rb[j][e] = (uint32_t)q[(int64_t)min(k0 + 2 * e, K - 1) * N] |
+                     ((uint32_t)q[(int64_t)min(k0 + 2 * e + 1, K - 1) * N] << 16);
+      }
     }
   }
 }
 
-template <int TM, int TN>
-__device__ __forceinline__ void dot_f32_mask(int kb, int g, int K, const float (&ra)[TM][8], const float (&rb)[TN][8],
-                                             float (&a)[TM][8], float (&bv)[TN][8]) {
+template <int KIND, int TM, int TN>
+__device__ __forceinline__ void dot_mm_mask(int kb, int g, int K, const uint32_t (&ra)[TM][8], const uint32_t (&rb)[TN][8],
+                                            uint32_t (&a)[TM][8], uint32_t (&bv)[TN][8]) {
   const int k0 = kb + 8 * g;
+  constexpr int W = KIND == kDkF32 ? 8 : 4;  // words per tile; a half word is valid as a whole
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const bool v = k0 + t < K;
+  for (int t = 0; t < W; ++t) {
+    const bool v = KIND == kDkF32 ? k0 + t < K : k0 < K;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) a[i][t] = v ? ra[i][t] : 0.f;
+    for (int i = 0; i < TM; ++i) a[i][t] = v ? ra[i][t] : 0u;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bv[j][t] = v ? rb[j][t] : 0.f;
+    for (int j = 0; j < TN; ++j) bv[j][t] = v ? rb[j][t] : 0u;
   }
 }
 
-template <bool BT, int WM, int WN, int TM, int TN>
-__global__ __launch_bounds__(256) void dot_f32_mfma_kernel(const float* __restrict__ lhs, const float* __restrict__ rhs,
-                                                           float* __restrict__ out, int M, int K, int N) {
+template <int KIND>
+__device__ __forceinline__ f32x4_t dot_mm_step(const uint32_t (&a)[8], const uint32_t (&b)[8], f32x4_t c) {
+  if constexpr (KIND == kDkF32) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[t]), __uint_as_float(b[t]), c, 0, 0, 0);
+    return c;
+  } else {
+    const u32x4_t av{a[0], a[1], a[2], a[3]}, bw{b[0], b[1], b[2], b[3]};
+    if constexpr (KIND == kDkBf16)
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, av), __builtin_bit_cast(bf16x8_v, bw), c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, av), __builtin_bit_cast(f16x8_v, bw), c, 0, 0, 0);
+  }
+}
+
+// out_half: 0 stores f32; otherwise the output is the input's half dtype, rounded once to
+// nearest even.
+template <int KIND, bool BT, int WM, int WN, int TM, int TN>
+__global__ __launch_bounds__(256) void dot_mm_kernel(const void* __restrict__ lhs, const void* __restrict__ rhs,
+                                                     void* __restrict__ out, int M, int K, int N, int out_half) {
   constexpr int KS = 4 / (WM * WN);
+  constexpr int ES = KIND == kDkF32 ? 4 : 2;  // input element bytes
   static_assert(KS * WM * WN == 4, "4 waves");
   __shared__ f32x4_t red[KS > 1 ? (KS - 1) * WM * WN * TM * TN * 64 : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -166,38 +217,36 @@ __global__ __launch_bounds__(256) void dot_f32_mfma_kernel(const float* __restri
   const int64_t bz = blockIdx.z;
   const int m0 = blockIdx.y * (16 * TM * WM) + wm * 16 * TM;
   const int n0 = blockIdx.x * (16 * TN * WN) + wn * 16 * TN;
-  const float* L = lhs + bz * M * K;
-  const float* R = rhs + bz * K * N;
-  const float* ap[TM];
-  const float* bp[TN];
+  const char* L = (const char*)lhs + bz * M * K * ES;
+  const char* R = (const char*)rhs + bz * K * N * ES;
+  const void* ap[TM];
+  const void* bp[TN];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) ap[i] = L + (int64_t)min(m0 + 16 * i + r, M - 1) * K;
+  for (int i = 0; i < TM; ++i) ap[i] = L + (int64_t)min(m0 + 16 * i + r, M - 1) * K * ES;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = min(n0 + 16 * j + r, N - 1);
-    bp[j] = BT ? R + (int64_t)n * K : R + n;
+    bp[j] = BT ? R + (int64_t)n * K * ES : R + (int64_t)n * ES;
   }
   f32x4_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int steps = (K + kF32Step - 1) / kF32Step;
-  float ra[TM][8], rb[TN][8];
-  dot_f32_load<BT, TM, TN>(ap, bp, wk * kF32Step, g, K, N, ra, rb);
+  const int steps = (K + kMmStep - 1) / kMmStep;
+  uint32_t ra[TM][8], rb[TN][8];
+  dot_mm_load<KIND, BT, TM, TN>(ap, bp, wk * kMmStep, g, K, N, ra, rb);
   for (int s = wk; s < steps; s += KS) {
-    float a[TM][8], bv[TN][8];
-    dot_f32_mask<TM, TN>(s * kF32Step, g, K, ra, rb, a, bv);
+    uint32_t a[TM][8], bv[TN][8];
+    dot_mm_mask<KIND, TM, TN>(s * kMmStep, g, K, ra, rb, a, bv);
     // Next step's operands (the last step reloads itself: in bounds, unused), issued ahead of
     // this step's products.
-    dot_f32_load<BT, TM, TN>(ap, bp, min(s + KS, steps - 1) * kF32Step, g, K, N, ra, rb);
+    dot_mm_load<KIND, BT, TM, TN>(ap, bp, min(s + KS, steps - 1) * kMmStep, g, K, N, ra, rb);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][t], bv[j][t], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < TN; ++j) acc[i][j] = dot_mm_step<KIND>(a[i], bv[j], acc[i][j]);
     __builtin_amdgcn_sched_barrier(0);
   }
   if constexpr (KS > 1) {
@@ -216,7 +265,6 @@ __global__ __launch_bounds__(256) void dot_f32_mfma_kernel(const float* __restri
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] += red[(((w - 1) * WM * WN + wmn) * TM * TN + i * TN + j) * 64 + lane];
   }
-  float* O = out + bz * M * N;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -225,42 +273,77 @@ __global__ __launch_bounds__(256) void dot_f32_mfma_kernel(const float* __restri
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + 16 * i + 4 * g + e;
-        if (m < M && n < N) O[(int64_t)m * N + n] = acc[i][j][e];
+        if (m >= M || n >= N) continue;
+        const int64_t o = bz * M * N + (int64_t)m * N + n;
+        const float v = acc[i][j][e];
+        if (!out_half)
+          ((float*)out)[o] = v;
+        else
+          ((uint16_t*)out)[o] = KIND == kDkBf16 ? f32_to_bf16(v) : f32_to_f16(v);
       }
     }
 }
 
-// Large enough f32 contractions (>= 2^20 multiply-adds) with K % 4 == 0 and 16-byte aligned
-// operands take the matrix cores; small ones keep the tiled kernel's sequential sums.
-static bool dot_f32_mfma_fits(const DotDesc& d) {
-  auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
-  return d.in_dt == MX_DTYPE_FLOAT32 && d.out_dt == MX_DTYPE_FLOAT32 && d.K >= 4 && d.K % 4 == 0 &&
-         d.B * d.M * d.N * d.K >= ((int64_t)1 << 20) && d.B <= 65535 && d.M < (1 << 24) && d.N < (1 << 24) &&
-         d.K < (1 << 24) && aligned(d.lhs, 16) && aligned(d.rhs, 16);
+static int dot_kind(int dt) {
+  return dt == MX_DTYPE_FLOAT32 ? kDkF32 : dt == MX_DTYPE_BFLOAT16 ? kDkBf16 : dt == MX_DTYPE_FLOAT16 ? kDkF16 : -1;
 }
 
-template <bool BT, int WM, int WN, int TM, int TN>
-static int dot_f32_mfma_launch(mx_backend* b, const DotDesc& d) {
+// Large enough contractions (>= 2^20 multiply-adds) with 16-byte aligned operands: f32 with
+// K % 4 == 0 (small ones keep the tiled kernel's sequential sums), half with K % 8 == 0 and f32
+// or half output.
+static bool dot_mm_fits(const DotDesc& d) {
+  auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
+  const int kind = dot_kind(d.in_dt);
+  if (kind < 0 || !(d.out_dt == MX_DTYPE_FLOAT32 || d.out_dt == d.in_dt)) return false;
+  const int kal = kind == kDkF32 ? 4 : 8;
+  return d.K >= kal && d.K % kal == 0 && d.B * d.M * d.N * d.K >= ((int64_t)1 << 20) && d.B <= 65535 &&
+         d.M < (1 << 24) && d.N < (1 << 24) && d.K < (1 << 24) && aligned(d.lhs, 16) && aligned(d.rhs, 16);
+}
+
+template <int KIND, bool BT, int WM, int WN, int TM, int TN>
+static int dot_mm_launch(mx_backend* b, const DotDesc& d, const char* name) {
   constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
   const dim3 grid((unsigned)((d.N + BN - 1) / BN), (unsigned)((d.M + BM - 1) / BM), (unsigned)d.B);
   if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "DotGeneral: M too large");
   hipStream_t st = b->stream;
-  return launch(b, "dot_mfma_f32", [&] {
-    dispatch(dot_f32_mfma_kernel<BT, WM, WN, TM, TN>, grid, 256, 0, st, (const float*)d.lhs, (const float*)d.rhs,
-             (float*)d.out, (int)d.M, (int)d.K, (int)d.N);
+  const int out_half = d.out_dt == MX_DTYPE_FLOAT32 ? 0 : 1;
+  return launch(b, name, [&] {
+    dispatch(dot_mm_kernel<KIND, BT, WM, WN, TM, TN>, grid, 256, 0, st, d.lhs, d.rhs, d.out, (int)d.M, (int)d.K, (int)d.N,
+             out_half);
   });
 }
 
 // Tile choice: the largest workgroup tile that still gives >= 512 workgroups; K-split waves
 // only when each has several K steps.
-template <bool BT>
-static int dot_f32_mfma_run(mx_backend* b, const DotDesc& d) {
+template <int KIND, bool BT>
+static int dot_mm_select(mx_backend* b, const DotDesc& d, const char* name) {
   auto wgs = [&](int bm, int bn) { return d.B * ((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn); };
-  const int64_t steps = (d.K + kF32Step - 1) / kF32Step;
-  if (wgs(64, 64) >= 512) return dot_f32_mfma_launch<BT, 2, 2, 2, 2>(b, d);
-  if (steps < 8) return dot_f32_mfma_launch<BT, 2, 2, 1, 1>(b, d);
-  if (wgs(32, 32) >= 512) return dot_f32_mfma_launch<BT, 1, 1, 2, 2>(b, d);
-  return dot_f32_mfma_launch<BT, 1, 1, 1, 2>(b, d);
+  const int64_t steps = (d.K + kMmStep - 1) / kMmStep;
+  if (wgs(64, 64) >= 512) return dot_mm_launch<KIND, BT, 2, 2, 2, 2>(b, d, name);
+  if (steps < 8) return dot_mm_launch<KIND, BT, 2, 2, 1, 1>(b, d, name);
+  if (wgs(32, 32) >= 512) return dot_mm_launch<KIND, BT, 1, 1, 2, 2>(b, d, name);
+  return dot_mm_launch<KIND, BT, 1, 1, 1, 2>(b, d, name);
+}
+
+static int dot_mm_run(mx_backend* b, const DotDesc& d) {
+  const bool bt = d.rhs_transposed;
+  switch (dot_kind(d.in_dt)) {
+    case kDkF32:
+      return bt ? dot_mm_select<kDkF32, true>(b, d, "dot_mfma_f32") : dot_mm_select<kDkF32, false>(b, d, "dot_mfma_f32");
+    case kDkBf16:
+      return bt ? dot_mm_select<kDkBf16, true>(b, d, "dot_mfma_bf16_tile")
+                : dot_mm_select<kDkBf16, false>(b, d, "dot_mfma_bf16_tile");
+    default:
+      return bt ? dot_mm_select<kDkF16, true>(b, d, "dot_mfma_f16_tile")
+                : dot_mm_select<kDkF16, false>(b, d, "dot_mfma_f16_tile");
+  }
+}
+
+// qdense_gemm.hip's 256x128-tile kernel takes half contractions that give it >= 64
+// workgroups (measured: at 96 it beats the small tiles 12 us to 22 us; at 24 or fewer the small
+// tiles win); smaller ones go to the small-tile kernel.
+static bool dot_big_tiles(const DotDesc& d) {
+  return dot_mfma_fits(d) && d.B * ((d.M + 255) / 256) * ((d.N + 127) / 128) >= 64;
 }
 
 int dot_run(mx_backend* b, const DotDesc& d) {
@@ -271,10 +354,11 @@ int dot_run(mx_backend* b, const DotDesc& d) {
     MX_CHECK_HIP(hipMemsetAsync(d.out, 0, bytes, b->stream));
     return MX_OK;
   }
+  if (dot_big_tiles(d))
+    return dot_mfma_run(b, d, d.in_dt == MX_DTYPE_BFLOAT16 ? "dot_mfma_bf16" : "dot_mfma_f16");
+  if (dot_mm_fits(d)) return dot_mm_run(b, d);
   if (dot_mfma_fits(d))
     return dot_mfma_run(b, d, d.in_dt == MX_DTYPE_BFLOAT16 ? "dot_mfma_bf16" : "dot_mfma_f16");
-  if (dot_f32_mfma_fits(d))
-    return d.rhs_transposed ? dot_f32_mfma_run<true>(b, d) : dot_f32_mfma_run<false>(b, d);
   if (dtype_is_half(d.in_dt) && d.out_dt != MX_DTYPE_FLOAT32) {
     // Half output folded in by the graph compiler, on a path that sums into f32 memory: the f32
     // result goes to a temporary, then ConvertDType's own kernel rounds it (the same arithmetic).

@@ -193,12 +193,22 @@ def _half(rng, shape, dt):
     return h, h.astype(np.float32)
 
 
+def _half_kernel(dt, shape):
+    """The half-precision kernel dot.hip picks: qdense_gemm.hip's 256x128 tiles when K % 64 == 0,
+    N % 16 == 0 and they give >= 64 workgroups, else the small-tile kernel."""
+    B, M, K, N = shape
+    name = "dot_mfma_bf16" if dt == ca.BFloat16 else "dot_mfma_f16"
+    big = K % 64 == 0 and N % 16 == 0 and B * -(-M // 256) * -(-N // 128) >= 64
+    return name if big else name + "_tile"
+
+
 @pytest.mark.parametrize("dt", [ca.BFloat16, ca.Float16])
 @pytest.mark.parametrize("transposed", [False, True])
-@pytest.mark.parametrize("shape", [(2, 300, 512, 272), (1, 1024, 1024, 1024), (3, 17, 4096, 256)])
+@pytest.mark.parametrize("shape", [(2, 300, 512, 272), (1, 1024, 1024, 1024), (3, 17, 4096, 256),
+                                   (1, 2048, 256, 4096), (2, 300, 1000, 270)])
 def test_mfma_dot_f32_accumulation(backend, dt, transposed, shape):
     """OutputDType f32: the matrix-core sums within 1e-5 of sum|terms| of the f64 value; the
-    kernel that ran is the matrix-core one."""
+    kernel that ran is the expected matrix-core one (large tiles or small tiles)."""
     B, M, K, N = shape
     rng = np.random.default_rng(B * 1000 + M + int(dt) + 3 * transposed)
     lhs, lv = _half(rng, (B, M, K), dt)
@@ -213,7 +223,7 @@ def test_mfma_dot_f32_accumulation(backend, dt, transposed, shape):
     finally:
         backend.SetProfiling(False)
     assert odt == ca.Float32
-    assert any(k.startswith("dot_mfma") for k in prof), prof
+    assert _half_kernel(dt, shape) in prof, prof
     truth = O.dot_general(lv.astype(np.float64), [2], [0], rv.astype(np.float64), rc, [0])
     scale = O.dot_general(np.abs(lv).astype(np.float64), [2], [0], np.abs(rv).astype(np.float64), rc, [0])
     assert np.all(np.abs(y.astype(np.float64) - truth) <= 1e-5 * scale)
@@ -288,3 +298,32 @@ def test_mfma_dot_f32_special_values_and_repeat(backend):
     truth = lhs[others].astype(np.float64) @ rhs.astype(np.float64)
     scale = np.abs(lhs[others]).astype(np.float64) @ rhs.astype(np.float64)
     assert np.all(np.abs(y1[others] - truth) <= 1e-5 * scale)
+
+
+@pytest.mark.parametrize("dt", [ca.BFloat16, ca.Float16])
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("shape", [(1, 2048, 1536, 384), (192, 128, 32, 128), (3, 77, 520, 130), (4, 130, 64, 70)])
+def test_mfma_dot_half_output_small_tiles(backend, dt, transposed, shape):
+    """Half inputs and output on the small-tile kernel (the bge-small projection and attention
+    shapes, and a ragged one with a K tail): f32 sums rounded once, rel 1e-2 / abs 1e-3 of the
+    f64 value; the bf16 result equals the f32-output result rounded to nearest even."""
+    B, M, K, N = shape
+    rng = np.random.default_rng(M * 13 + K + int(dt) + 3 * transposed)
+    lhs, lv = _half(rng, (B, M, K), dt)
+    rhs, rv = _half(rng, (B, N, K) if transposed else (B, K, N), dt)
+    rc = [2] if transposed else [1]
+    backend.ProfileReset()
+    backend.SetProfiling(True)
+    try:
+        y, odt = run(backend, [(lhs, dt), (rhs, dt)], lambda f, p: f.DotGeneral(p[0], [2], [0], p[1], rc, [0]))
+        prof = backend.Profile()
+    finally:
+        backend.SetProfiling(False)
+    assert odt == dt and _half_kernel(dt, shape) in prof, prof
+    truth = O.dot_general(lv.astype(np.float64), [2], [0], rv.astype(np.float64), rc, [0])
+    got = O.bf16_to_f32(y) if dt == ca.BFloat16 else y.astype(np.float32)
+    assert np.all(np.abs(got - truth) <= 1e-3 + 1e-2 * np.abs(truth))
+    y32, _ = run(backend, [(lhs, dt), (rhs, dt)],
+                 lambda f, p: f.DotGeneral(p[0], [2], [0], p[1], rc, [0], ca.DotGeneralConfig(OutputDType=ca.Float32)))
+    want = O.bf16_round(y32.astype(np.float32)) if dt == ca.BFloat16 else y32.astype(np.float32).astype(np.float16)
+    assert np.array_equal(y.view(np.uint16), want.view(np.uint16))
