@@ -284,6 +284,127 @@ __global__ __launch_bounds__(256) void dot_mm_kernel(const void* __restrict__ lh
     }
 }
 
+// LDS-staged variant for a transposed right-hand side ([N, K]; the normalized layout of every
+// projection in the reference's model benchmarks): a 64x64 tile per workgroup, its 4 waves 2x2
+// over 32x32, K steps of 32 staged through two LDS buffers.  All 256 threads load A and B
+// rows together, 8 (f32) or 4 (half) lanes per contiguous row segment, so each element is
+// loaded once per workgroup and each load instruction touches whole row segments; the waves
+// then read their fragments in the MFMA layout above (lane group g: k = 8g .. 8g+7) from rows
+// padded by 16 bytes, which keeps each 16-lane read on distinct banks.
+template <int KIND>
+__global__ __launch_bounds__(256) void dot_mm_lds_kernel(const void* __restrict__ lhs, const void* __restrict__ rhs,
+                                                         void* __restrict__ out, int M, int K, int N, int out_half) {
+  constexpr int ES = KIND == kDkF32 ? 4 : 2;
+  constexpr int RB = kMmStep * ES, RS = RB + 16;  // row bytes per step; padded LDS row stride
+  constexpr int LPR = RB / 16;                     // 16-byte chunks per row segment
+  constexpr int PASSES = 64 * LPR / 256;           // 16-byte loads per thread per operand
+  __shared__ __attribute__((aligned(16))) char sm[2][2][64 * RS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1, r = lane & 15, g = lane >> 4;
+  const int64_t bz = blockIdx.z;
+  const int mt = blockIdx.y * 64, nt = blockIdx.x * 64;
+  const char* L = (const char*)lhs + bz * M * K * ES;
+  const char* R = (const char*)rhs + bz * K * N * ES;
+  const int c = tid % LPR, row0 = tid / LPR;  // this thread's chunk and first row
+  const char* ga[PASSES];
+  const char* gb[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int row = row0 + p * (256 / LPR);
+    ga[p] = L + (int64_t)min(mt + row, M - 1) * K * ES;
+    gb[p] = R + (int64_t)min(nt + row, N - 1) * K * ES;
+  }
+  // Global loads run two K steps ahead of the products, in two register sets X and Y (even and
+  // odd steps) with the loop unrolled by two so both stay static.  Steps past the end load
+  // clamped addresses and store zeros (lstore's K mask), so an odd last pair adds nothing.
+  const int steps = (K + kMmStep - 1) / kMmStep;
+  u32x4_t xa[PASSES], xb[PASSES], ya[PASSES], yb[PASSES];
+  auto gload = [&](int s, u32x4_t (&va)[PASSES], u32x4_t (&vb)[PASSES]) {
+    // A chunk holds 4 (f32) or 8 (half) k: wholly inside K or wholly past it (K % 4 / K % 8);
+    // one past it loads the row's last chunk instead (in bounds) and is zeroed by lstore.
+    const int64_t off = (int64_t)min(s * kMmStep + c * (16 / ES), K - 16 / ES) * ES;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      va[p] = *(const u32x4_t*)(ga[p] + off);
+      vb[p] = *(const u32x4_t*)(gb[p] + off);
+    }
+  };
+  auto lstore = [&](int s, int buf, const u32x4_t (&va)[PASSES], const u32x4_t (&vb)[PASSES]) {
+    const bool v = s * kMmStep + c * (16 / ES) < K;
+    const u32x4_t z{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = row0 + p * (256 / LPR);
+      *(u32x4_t*)(&sm[buf][0][row * RS + c * 16]) = v ? va[p] : z;
+      *(u32x4_t*)(&sm[buf][1][row * RS + c * 16]) = v ? vb[p] : z;
+    }
+  };
+  f32x4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int buf) {
+    uint32_t a[2][8], bv[2][8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const char* pa = &sm[buf][0][(wm * 32 + 16 * i + r) * RS + g * 8 * ES];
+      const char* pb = &sm[buf][1][(wn * 32 + 16 * i + r) * RS + g * 8 * ES];
+#pragma unroll
+      for (int h = 0; h < 8 * ES / 16; ++h) {
+        const u32x4_t x = *(const u32x4_t*)(pa + 16 * h), y = *(const u32x4_t*)(pb + 16 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a[i][4 * h + e] = x[e];
+          bv[i][4 * h + e] = y[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = dot_mm_step<KIND>(a[i], bv[j], acc[i][j]);
+  };
+  // The scheduling barriers keep each set's loads where they are issued, so a store waits only
+  // for the older set.
+  gload(0, xa, xb);
+  __builtin_amdgcn_sched_barrier(0);
+  gload(1, ya, yb);
+  __builtin_amdgcn_sched_barrier(0);
+  lstore(0, 0, xa, xb);
+  __syncthreads();
+  for (int s = 0; s < steps; s += 2) {
+    gload(s + 2, xa, xb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0);
+    lstore(s + 1, 1, ya, yb);
+    __syncthreads();
+    gload(s + 3, ya, yb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);
+    lstore(s + 2, 0, xa, xb);
+    __syncthreads();
+  }
+  const int m0 = mt + wm * 32, n0 = nt + wn * 32;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 16 * j + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 16 * i + 4 * g + e;
+        if (m >= M || n >= N) continue;
+        const int64_t o = bz * M * N + (int64_t)m * N + n;
+        const float v = acc[i][j][e];
+        if (!out_half)
+          ((float*)out)[o] = v;
+        else
+          ((uint16_t*)out)[o] = KIND == kDkBf16 ? f32_to_bf16(v) : f32_to_f16(v);
+      }
+    }
+}
+
 static int dot_kind(int dt) {
   return dt == MX_DTYPE_FLOAT32 ? kDkF32 : dt == MX_DTYPE_BFLOAT16 ? kDkBf16 : dt == MX_DTYPE_FLOAT16 ? kDkF16 : -1;
 }
@@ -313,11 +434,26 @@ static int dot_mm_launch(mx_backend* b, const DotDesc& d, const char* name) {
   });
 }
 
-// Tile choice: the largest workgroup tile that still gives >= 512 workgroups; K-split waves
-// only when each has several K steps.
+template <int KIND>
+static int dot_mm_lds_launch(mx_backend* b, const DotDesc& d, const char* name) {
+  const dim3 grid((unsigned)((d.N + 63) / 64), (unsigned)((d.M + 63) / 64), (unsigned)d.B);
+  if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "DotGeneral: M too large");
+  hipStream_t st = b->stream;
+  const int out_half = d.out_dt == MX_DTYPE_FLOAT32 ? 0 : 1;
+  return launch(b, name, [&] {
+    dispatch(dot_mm_lds_kernel<KIND>, grid, 256, 0, st, d.lhs, d.rhs, d.out, (int)d.M, (int)d.K, (int)d.N, out_half);
+  });
+}
+
+// Tile choice: a transposed right-hand side with >= 128 64x64 tiles stages them through LDS;
+// otherwise the largest register tile that still gives >= 512 workgroups, K-split waves only
+// when each has several K steps.
 template <int KIND, bool BT>
 static int dot_mm_select(mx_backend* b, const DotDesc& d, const char* name) {
   auto wgs = [&](int bm, int bn) { return d.B * ((d.M + bm - 1) / bm) * ((d.N + bn - 1) / bn); };
+  if constexpr (BT) {
+    if (wgs(64, 64) >= 128) return dot_mm_lds_launch<KIND>(b, d, name);
+  }
   const int64_t steps = (d.K + kMmStep - 1) / kMmStep;
   if (wgs(64, 64) >= 512) return dot_mm_launch<KIND, BT, 2, 2, 2, 2>(b, d, name);
   if (steps < 8) return dot_mm_launch<KIND, BT, 2, 2, 1, 1>(b, d, name);
