@@ -6,8 +6,8 @@
 // The tiled kernel stages 64x64 output tiles through LDS, 16-deep in K, each thread owning a
 // 4x4 register block; it serves f64, small or unaligned f32 (accumulating in the input type)
 // and small bf16/f16 (accumulating in f32).  Larger contractions run on the matrix cores: the
-// small-tile dot_mm_kernel below (f32, and half problems too small for qdense_gemm.hip's
-// 256x128-tile kernel), or that kernel.
+// small-tile dot_mm_kernel / dot_mm_lds_kernel below (f32, and half problems too small for
+// qdense_gemm.hip's 256x128-tile kernel), or that kernel.
 
 #include "device_common.h"
 #include "mxrt_internal.h"
@@ -290,16 +290,19 @@ __global__ __launch_bounds__(256) void dot_mm_kernel(const void* __restrict__ lh
 // rows together, 8 (f32) or 4 (half) lanes per contiguous row segment, so each element is
 // loaded once per workgroup and each load instruction touches whole row segments; the waves
 // then read their fragments in the MFMA layout above (lane group g: k = 8g .. 8g+7) from rows
-// padded by 16 bytes, which keeps each 16-lane read on distinct banks.
-template <int KIND>
-__global__ __launch_bounds__(256) void dot_mm_lds_kernel(const void* __restrict__ lhs, const void* __restrict__ rhs,
-                                                         void* __restrict__ out, int M, int K, int N, int out_half) {
+// padded by 16 bytes, which keeps each 16-lane read on distinct banks.  With KS2 = 2 the
+// workgroup has 8 waves: each half (256 threads) loads and multiplies alternate K steps, and
+// the halves' sums are added through LDS at the end (two waves per SIMD when the grid has
+// fewer tiles than CUs).
+template <int KIND, int KS2>
+__global__ __launch_bounds__(256 * KS2) void dot_mm_lds_kernel(const void* __restrict__ lhs, const void* __restrict__ rhs,
+                                                               void* __restrict__ out, int M, int K, int N, int out_half) {
   constexpr int ES = KIND == kDkF32 ? 4 : 2;
   constexpr int RB = kMmStep * ES, RS = RB + 16;  // row bytes per step; padded LDS row stride
   constexpr int LPR = RB / 16;                     // 16-byte chunks per row segment
   constexpr int PASSES = 64 * LPR / 256;           // 16-byte loads per thread per operand
-  __shared__ __attribute__((aligned(16))) char sm[2][2][64 * RS];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ __attribute__((aligned(16))) char sm[2][KS2][2][64 * RS];
+  const int part = threadIdx.x >> 8, tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1, r = lane & 15, g = lane >> 4;
   const int64_t bz = blockIdx.z;
   const int mt = blockIdx.y * 64, nt = blockIdx.x * 64;
@@ -322,7 +325,7 @@ __global__ __launch_bounds__(256) void dot_mm_lds_kernel(const void* __restrict_
   auto gload = [&](int s, u32x4_t (&va)[PASSES], u32x4_t (&vb)[PASSES]) {
     // A chunk holds 4 (f32) or 8 (half) k: wholly inside K or wholly past it (K % 4 / K % 8);
     // one past it loads the row's last chunk instead (in bounds) and is zeroed by lstore.
-    const int64_t off = (int64_t)min(s * kMmStep + c * (16 / ES), K - 16 / ES) * ES;
+    const int64_t off = (int64_t)min((s * KS2 + part) * kMmStep + c * (16 / ES), K - 16 / ES) * ES;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       va[p] = *(const u32x4_t*)(ga[p] + off);
@@ -330,13 +333,13 @@ __global__ __launch_bounds__(256) void dot_mm_lds_kernel(const void* __restrict_
     }
   };
   auto lstore = [&](int s, int buf, const u32x4_t (&va)[PASSES], const u32x4_t (&vb)[PASSES]) {
-    const bool v = s * kMmStep + c * (16 / ES) < K;
+    const bool v = (s * KS2 + part) * kMmStep + c * (16 / ES) < K;
     const u32x4_t z{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int row = row0 + p * (256 / LPR);
-      *(u32x4_t*)(&sm[buf][0][row * RS + c * 16]) = v ? va[p] : z;
-      *(u32x4_t*)(&sm[buf][1][row * RS + c * 16]) = v ? vb[p] : z;
+      *(u32x4_t*)(&sm[buf][part][0][row * RS + c * 16]) = v ? va[p] : z;
+      *(u32x4_t*)(&sm[buf][part][1][row * RS + c * 16]) = v ? vb[p] : z;
     }
   };
   f32x4_t acc[2][2];
@@ -348,8 +351,8 @@ __global__ __launch_bounds__(256) void dot_mm_lds_kernel(const void* __restrict_
     uint32_t a[2][8], bv[2][8];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const char* pa = &sm[buf][0][(wm * 32 + 16 * i + r) * RS + g * 8 * ES];
-      const char* pb = &sm[buf][1][(wn * 32 + 16 * i + r) * RS + g * 8 * ES];
+      const char* pa = &sm[buf][part][0][(wm * 32 + 16 * i + r) * RS + g * 8 * ES];
+      const char* pb = &sm[buf][part][1][(wn * 32 + 16 * i + r) * RS + g * 8 * ES];
 #pragma unroll
       for (int h = 0; h < 8 * ES / 16; ++h) {
         const u32x4_t x = *(const u32x4_t*)(pa + 16 * h), y = *(const u32x4_t*)(pb + 16 * h);
@@ -365,6 +368,7 @@ __global__ __launch_bounds__(256) void dot_mm_lds_kernel(const void* __restrict_
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = dot_mm_step<KIND>(a[i], bv[j], acc[i][j]);
   };
+  const int nq = (steps + KS2 - 1) / KS2;  // step groups (one step per half)
   // The scheduling barriers keep each set's loads where they are issued, so a store waits only
   // for the older set.
   gload(0, xa, xb);
@@ -373,7 +377,7 @@ __global__ __launch_bounds__(256) void dot_mm_lds_kernel(const void* __restrict_
   __builtin_amdgcn_sched_barrier(0);
   lstore(0, 0, xa, xb);
   __syncthreads();
-  for (int s = 0; s < steps; s += 2) {
+  for (int s = 0; s < nq; s += 2) {
     gload(s + 2, xa, xb);
     __builtin_amdgcn_sched_barrier(0);
     compute(0);
@@ -384,6 +388,22 @@ __global__ __launch_bounds__(256) void dot_mm_lds_kernel(const void* __restrict_
     compute(1);
     lstore(s + 2, 0, xa, xb);
     __syncthreads();
+  }
+  if constexpr (KS2 > 1) {
+    // The loop ended on a barrier: the LDS buffers are free.  Half 1 hands its sums to half 0.
+    f32x4_t* red = (f32x4_t*)&sm[0][0][0][0];
+    if (part == 1) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) red[(wave * 4 + i * 2 + j) * 64 + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (part == 1) return;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] += red[(wave * 4 + i * 2 + j) * 64 + lane];
   }
   const int m0 = mt + wm * 32, n0 = nt + wn * 32;
 #pragma unroll
@@ -440,8 +460,13 @@ static int dot_mm_lds_launch(mx_backend* b, const DotDesc& d, const char* name) 
   if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "DotGeneral: M too large");
   hipStream_t st = b->stream;
   const int out_half = d.out_dt == MX_DTYPE_FLOAT32 ? 0 : 1;
+  // Fewer tiles than CUs and several K steps: 8 waves splitting K.
+  const bool split = (int64_t)grid.x * grid.y * grid.z < 256 && d.K >= 8 * kMmStep;
   return launch(b, name, [&] {
-    dispatch(dot_mm_lds_kernel<KIND>, grid, 256, 0, st, d.lhs, d.rhs, d.out, (int)d.M, (int)d.K, (int)d.N, out_half);
+    if (split)
+      dispatch(dot_mm_lds_kernel<KIND, 2>, grid, 512, 0, st, d.lhs, d.rhs, d.out, (int)d.M, (int)d.K, (int)d.N, out_half);
+    else
+      dispatch(dot_mm_lds_kernel<KIND, 1>, grid, 256, 0, st, d.lhs, d.rhs, d.out, (int)d.M, (int)d.K, (int)d.N, out_half);
   });
 }
 

@@ -249,14 +249,15 @@ def test_mfma_dot_half_output_and_prefill_shape(backend, dt):
 # ---------------------------------------------------------------------------------------------
 # f32 DotGeneral on the matrix cores (dot.hip, dot_mfma_f32: v_mfma_f32_16x16x4_f32, fp32
 # products and sums): contractions of >= 2^20 multiply-adds with K % 4 == 0.  The shapes reach
-# every tile configuration (64x64, 32x32 with K split over the waves, 16x32, 32x32 for short K),
-# ragged M and N, K tails inside a 32-deep step, M below one 16-row tile, and the reference's
-# MiniLM projection shape [32*13, 1536] x [1536, 384] (bench_dotgeneral.go).
+# every tile configuration (64x64, 32x32 with K split over the waves, 16x32, 32x32 for short K;
+# transposed: the LDS-staged 64x64 tiles, 4 waves or 8 waves splitting K), ragged M and N, K
+# tails inside a 32-deep step and an odd number of steps, M below one 16-row tile, and the
+# reference's MiniLM and bge-small projection shapes (bench_dotgeneral.go).
 # ---------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("transposed", [False, True])
 @pytest.mark.parametrize("shape", [(1, 416, 1536, 384), (2, 300, 1000, 272), (1, 1024, 1024, 1024),
                                    (2, 130, 64, 70), (1, 2048, 512, 1024), (192, 128, 32, 128), (1, 5, 4096, 520),
-                                   (3, 777, 36, 1030)])
+                                   (3, 777, 36, 1030), (1, 1920, 1536, 384), (1, 640, 1028, 1500)])
 def test_mfma_dot_f32(backend, transposed, shape):
     """Within 1e-5 of sum|terms| of the f64 value (only the summation order differs from a
     sequential f32 sum), and the kernel that ran is the matrix-core one."""
