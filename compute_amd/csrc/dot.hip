@@ -500,11 +500,11 @@ static int dot_mm_run(mx_backend* b, const DotDesc& d) {
   }
 }
 
-// qdense_gemm.hip's 256x128-tile kernel takes half contractions that give it >= 64
-// workgroups (measured: at 96 it beats the small tiles 12 us to 22 us; at 24 or fewer the small
-// tiles win); smaller ones go to the small-tile kernel.
+// qdense_gemm.hip's 256x128-tile kernel takes half contractions with M >= 256 that give it
+// >= 64 workgroups (measured: at 96 it beats the small tiles 12 us to 22 us; at 24 or fewer,
+// or batched with M = 128 / 192, the small tiles win); others go to the small-tile kernels.
 static bool dot_big_tiles(const DotDesc& d) {
-  return dot_mfma_fits(d) && d.B * ((d.M + 255) / 256) * ((d.N + 127) / 128) >= 64;
+  return dot_mfma_fits(d) && d.M >= 256 && d.B * ((d.M + 255) / 256) * ((d.N + 127) / 128) >= 64;
 }
 
 int dot_run(mx_backend* b, const DotDesc& d) {

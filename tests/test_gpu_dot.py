@@ -195,10 +195,10 @@ def _half(rng, shape, dt):
 
 def _half_kernel(dt, shape):
     """The half-precision kernel dot.hip picks: qdense_gemm.hip's 256x128 tiles when K % 64 == 0,
-    N % 16 == 0 and they give >= 64 workgroups, else the small-tile kernel."""
+    N % 16 == 0, M >= 256 and they give >= 64 workgroups, else the small-tile kernel."""
     B, M, K, N = shape
     name = "dot_mfma_bf16" if dt == ca.BFloat16 else "dot_mfma_f16"
-    big = K % 64 == 0 and N % 16 == 0 and B * -(-M // 256) * -(-N // 128) >= 64
+    big = K % 64 == 0 and N % 16 == 0 and M >= 256 and B * -(-M // 256) * -(-N // 128) >= 64
     return name if big else name + "_tile"
 
 
