@@ -272,6 +272,28 @@ __global__ void gather_kernel(const T* __restrict__ in, T* __restrict__ out, Gat
   }
 }
 
+// Gathers whose innermost output axis reads contiguous input (stride 1, 64..4096 elements; the
+// axis moves of DotGeneral's normalization and most transposes): one wave per output row works
+// out the row's source offset once and its lanes copy the row, instead of a div/mod chain per
+// element.  Shorter rows leave too many lanes idle (measured slower at 32) and stay per element.
+template <typename T>
+__global__ void gather_rows_kernel(const T* __restrict__ in, T* __restrict__ out, GatherDims d, int64_t rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t L = d.out[d.rank - 1];
+  const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  for (int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); r < rows; r += waves) {
+    int64_t rem = r, src = d.offset;
+    for (int a = d.rank - 2; a >= 0; --a) {
+      const int64_t c = rem % d.out[a];
+      rem /= d.out[a];
+      src += c * d.st[a];
+    }
+    const T* s = in + src;
+    T* o = out + r * L;
+    for (int64_t j = lane; j < L; j += 64) o[j] = s[j];
+  }
+}
+
 int ew_gather_strided(mx_backend* b, const void* in, void* out, int elem_bytes, const int64_t* out_dims,
                       const int64_t* in_strides, int64_t in_offset, int rank) {
   GatherDims d{};
@@ -285,6 +307,18 @@ int ew_gather_strided(mx_backend* b, const void* in, void* out, int elem_bytes, 
   }
   if (n == 0) return MX_OK;
   hipStream_t st = b->stream;
+  const int64_t L = rank > 0 ? out_dims[rank - 1] : 1;
+  if (rank >= 2 && in_strides[rank - 1] == 1 && L >= 64 && L <= 4096) {
+    const int64_t rows = n / L;
+    const unsigned blocks = ew_blocks(rows * 64);
+    switch (elem_bytes) {
+      case 1: return launch(b, "gather_rows", [&] { dispatch(gather_rows_kernel<uint8_t>, blocks, kEwThreads, 0, st, (const uint8_t*)in, (uint8_t*)out, d, rows); });
+      case 2: return launch(b, "gather_rows", [&] { dispatch(gather_rows_kernel<uint16_t>, blocks, kEwThreads, 0, st, (const uint16_t*)in, (uint16_t*)out, d, rows); });
+      case 4: return launch(b, "gather_rows", [&] { dispatch(gather_rows_kernel<uint32_t>, blocks, kEwThreads, 0, st, (const uint32_t*)in, (uint32_t*)out, d, rows); });
+      case 8: return launch(b, "gather_rows", [&] { dispatch(gather_rows_kernel<uint64_t>, blocks, kEwThreads, 0, st, (const uint64_t*)in, (uint64_t*)out, d, rows); });
+      default: break;
+    }
+  }
   switch (elem_bytes) {
     case 1: return launch(b, "gather", [&] { dispatch(gather_kernel<uint8_t>, ew_blocks(n), kEwThreads, 0, st, (const uint8_t*)in, (uint8_t*)out, d, n); });
     case 2: return launch(b, "gather", [&] { dispatch(gather_kernel<uint16_t>, ew_blocks(n), kEwThreads, 0, st, (const uint16_t*)in, (uint16_t*)out, d, n); });

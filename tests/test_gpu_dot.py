@@ -328,3 +328,40 @@ def test_mfma_dot_half_output_small_tiles(backend, dt, transposed, shape):
                  lambda f, p: f.DotGeneral(p[0], [2], [0], p[1], rc, [0], ca.DotGeneralConfig(OutputDType=ca.Float32)))
     want = O.bf16_round(y32.astype(np.float32)) if dt == ca.BFloat16 else y32.astype(np.float32).astype(np.float16)
     assert np.array_equal(y.view(np.uint16), want.view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------------------
+# Data movement behind DotGeneral's axis normalization (elementwise.hip): a gather whose
+# innermost output axis reads contiguous input of 64..4096 elements copies whole rows
+# (gather_rows), any other one indexes element by element.  Both are exact copies.
+# ---------------------------------------------------------------------------------------------
+_MOVE_DTYPES = [(ca.Float32, np.float32), (ca.BFloat16, np.uint16), (ca.Float64, np.float64), (ca.Int8, np.int8)]
+
+
+@pytest.mark.parametrize("dt,npt", _MOVE_DTYPES)
+@pytest.mark.parametrize("perm", [(0, 2, 1, 3), (2, 0, 1, 3), (0, 1, 3, 2), (3, 2, 1, 0)])
+def test_transpose_exact(backend, dt, npt, perm):
+    rng = np.random.default_rng(sum(perm) * 31 + int(dt))
+    x = (rng.standard_normal((5, 37, 6, 72)) * 50).astype(npt) if npt != np.uint16 else \
+        rng.integers(0, 1 << 16, (5, 37, 6, 72), dtype=np.uint16)
+    backend.ProfileReset()
+    backend.SetProfiling(True)
+    try:
+        y, odt = run(backend, [(x, dt)], lambda f, p: f.Transpose(p[0], *perm))
+        prof = backend.Profile()
+    finally:
+        backend.SetProfiling(False)
+    assert odt == dt
+    assert np.array_equal(y.view(np.uint8), np.ascontiguousarray(np.transpose(x, perm)).view(np.uint8))
+    assert ("gather_rows" in prof) == (perm[-1] == 3), prof
+
+
+@pytest.mark.parametrize("strides", [None, [1, 2, 1, 1], [1, 1, 1, 2]])
+def test_slice_exact(backend, strides):
+    """Slices with an offset: unit inner stride takes the row copy, a strided inner axis not."""
+    x = np.arange(5 * 37 * 6 * 100, dtype=np.float32).reshape(5, 37, 6, 100)
+    starts, limits = [1, 2, 0, 5], [4, 30, 6, 90]
+    y, _ = run(backend, [(x, ca.Float32)], lambda f, p: f.Slice(p[0], starts, limits, strides))
+    st = strides or [1, 1, 1, 1]
+    want = x[tuple(slice(a, b, c) for a, b, c in zip(starts, limits, st))]
+    assert np.array_equal(y, want)
