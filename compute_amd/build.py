@@ -28,9 +28,14 @@ COMMON = [
 SOURCES = ["runtime.cpp", "graph.cpp", "qdense.hip", "qdense_skinny.hip", "qdense_gemv.hip", "qdense_gemm.hip", "ggml.hip", "dot.hip", "elementwise.hip"]
 
 
+# The skinny kernel takes one arrival ticket per workgroup from a single lane; LLVM's atomic
+# optimizer would turn that atomic into a wave-wide one whose result is waited for at once.
+EXTRA = {"qdense_skinny.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
+
+
 def _compile(src: str) -> Path:
     out = OBJ / (src + ".o")
-    cmd = [HIPCC, *COMMON, "-x", "hip", "-c", str(CSRC / src), "-o", str(out)]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src, []), "-x", "hip", "-c", str(CSRC / src), "-o", str(out)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")
@@ -41,7 +46,7 @@ def build(verbose: bool = False) -> Path:
     """Compiles every source (always) and links libmxrt.so; returns the library path."""
     OBJ.mkdir(parents=True, exist_ok=True)
     LIB.parent.mkdir(parents=True, exist_ok=True)
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(os.cpu_count() or 8, len(SOURCES))) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]

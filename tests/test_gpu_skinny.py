@@ -96,3 +96,40 @@ def test_skinny_mlp_gate_shape(backend):
         r = QDenseRun(backend, p)
         assert r.plan() == "qdense_skinny_mfma_i4"
         check(r, threads=8, what=f"MLP {K}x{N}")
+
+
+# Shapes around the split-K decomposition: one or many column blocks, K from one step to deep
+# slices, a partial last column block, and the headline C2 / MLP shapes.
+PARTITION_SHAPES = [
+    (1, 64, 256, 32),
+    (2, 1024, 512, 128),
+    (1, 8192, 256, 128),
+    (3, 2080, 1024, 32),
+    (1, 4096, 11008, 128),
+    (8, 14336, 4096, 128),
+]
+
+
+@pytest.mark.parametrize("shape", PARTITION_SHAPES)
+@pytest.mark.parametrize("w_dtype", [O.DT_INT4, O.DT_UINT8])
+def test_skinny_partitions(backend, shape, w_dtype):
+    M, K, N, G = shape
+    p = O.make_problem(M, K, N, w_dtype=w_dtype, block_axis=0, block_size=G, bias=True, act=O.ACT_NONE,
+                       scale_range=(0.002, 0.02), seed=K + N + M)
+    r = QDenseRun(backend, p)
+    assert r.plan().startswith("qdense_skinny_mfma")
+    check(r, threads=8, what=f"{shape} {w_dtype}")
+
+
+def test_skinny_shape_sequence(backend):
+    """Calls of different shapes share the backend's split-K scratch (arrival counters and partial
+    tiles): alternating shapes, each call checked, each repeated call equal."""
+    probs = [O.make_problem(M, K, N, w_dtype=O.DT_INT4, block_axis=0, block_size=128, bias=False, seed=s)
+             for s, (M, K, N) in enumerate([(1, 4096, 2048), (16, 1024, 4096), (4, 8192, 512)])]
+    runs = [QDenseRun(backend, p) for p in probs]
+    first = [r.run() for r in runs]
+    for r, y in zip(runs, first):
+        assert_bf16_close(y, O.qdense_f32(r.p, threads=8), what=f"{r.p.M}x{r.p.K}x{r.p.N}")
+    for _ in range(2):
+        for r, y in zip(runs[::-1], first[::-1]):
+            assert np.array_equal(r.run(), y)
