@@ -95,29 +95,89 @@ def mfma_roofline(flops: float, us: float, traffic):
             "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic}
 
 
-def cpu_baseline(wl, seconds: float):
-    """The oracle (plain-C restatement of quantizedDenseLinearInt, parallel like the reference's
-    quantizedDenseParallel) timed on this host over a bounded sample of the same workload."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _oracle_problems(wl):
+    """The workload as oracle problems: one for a FusedQuantizedDense workload, the three
+    projections (gate, up, down) for the MLP, whose other ops are a few KB of elementwise work."""
+    import numpy as np
     from oracle import oracle as O
 
-    dtmap = {"Int8": O.DT_INT8, "Int4": O.DT_INT4, "Float32": O.DT_FLOAT32, "BFloat16": O.DT_BFLOAT16}
-    p = O.QDenseProblem(M=wl.M, K=wl.K, N=wl.N, x=wl.x, x_dtype=dtmap[str(wl.x_dtype)], w=wl.w,
-                        w_dtype=dtmap[str(wl.w_dtype)], scale=wl.scale, scale_dtype=dtmap[str(wl.scale_dtype)],
-                        scale_shape=wl.scale_shape, block_axis=wl.block_axis, block_size=wl.block_size,
-                        bias=wl.bias, bias_dtype=dtmap[str(wl.bias_dtype)] if wl.bias is not None else O.DT_FLOAT32,
-                        act=wl.act)
-    threads = min(16, os.cpu_count() or 1)
-    O.qdense_f32(p, threads=threads)  # warm up
+    dtmap = {"Int8": O.DT_INT8, "Int4": O.DT_INT4, "Uint4": O.DT_UINT4, "Float32": O.DT_FLOAT32,
+             "BFloat16": O.DT_BFLOAT16}
+    if hasattr(wl, "weights"):
+        h = wl.x  # RMSNorm output stand-in of the same shape and dtype (timing only)
+        return [O.QDenseProblem(M=wl.M, K=K, N=N, x=h if K == wl.D else np.zeros((wl.M, K), np.uint16),
+                                x_dtype=O.DT_BFLOAT16, w=w, w_dtype=O.DT_INT4, scale=sc, scale_dtype=O.DT_BFLOAT16,
+                                scale_shape=(K // wl.G, N), block_axis=0, block_size=wl.G, bias=None,
+                                bias_dtype=O.DT_FLOAT32, act=0)
+                for w, sc, K, N in wl.weights]
+    return [O.QDenseProblem(M=wl.M, K=wl.K, N=wl.N, x=wl.x, x_dtype=dtmap[str(wl.x_dtype)], w=wl.w,
+                            w_dtype=dtmap[str(wl.w_dtype)], scale=wl.scale, scale_dtype=dtmap[str(wl.scale_dtype)],
+                            scale_shape=wl.scale_shape, block_axis=wl.block_axis, block_size=wl.block_size,
+                            bias=wl.bias,
+                            bias_dtype=dtmap[str(wl.bias_dtype)] if wl.bias is not None else O.DT_FLOAT32,
+                            act=wl.act, scheme=wl.scheme)]
+
+
+def cpu_time_per_call(wl, seconds: float, threads: int):
+    """Seconds per full call of the oracle on `threads` threads, from a bounded sample: whole
+    calls, or for large M a block of rows scaled up to M (the loop is row-independent)."""
+    import numpy as np
+    from oracle import oracle as O
+
+    probs = _oracle_problems(wl)
+    rows = None
+    if wl.M > 64:
+        rows = np.arange(0, wl.M, wl.M // 16, dtype=np.int64)[:16]
+    for p in probs:  # warm up
+        O.qdense_f32(p, rows=rows, threads=threads)
     calls, t0 = 0, time.perf_counter()
     while True:
-        O.qdense_f32(p, threads=threads)
+        for p in probs:
+            O.qdense_f32(p, rows=rows, threads=threads)
         calls += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    gbs = wl.algorithmic_bytes() * calls / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{calls} full calls of {wl.name} in {el:.1f} s ({el / calls * 1e3:.2f} ms/call)"}
+    per = el / calls
+    if rows is not None:
+        per *= wl.M / len(rows)
+    what = f"{calls} calls" + (f" of {len(rows)} of {wl.M} rows, scaled to all rows" if rows is not None else "")
+    return per, what
+
+
+def cpu_baseline(headline, others, seconds: float):
+    """The oracle (plain-C restatement of quantizedDenseLinearInt, quantizeddense.go:616-650, run
+    in parallel over output rows and columns like quantizedDenseParallel) timed on this host's
+    cores, since the reference's Go toolchain is absent: the headline config gives `value`, every
+    config its own entry."""
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    per, what = cpu_time_per_call(headline, seconds, threads)
+    out = {"value": round(headline.algorithmic_bytes() / per / 1e9, 3), "unit": "GB/s", "cores": threads,
+           "nproc": os.cpu_count(), "cpu_model": _cpu_model(), "kind": "port",
+           "sample": f"{what} of {headline.name} in the C oracle ({per * 1e3:.2f} ms/call); Go (gobackend) "
+                     "is absent from this image, so the oracle's restatement of quantizeddense.go:616-650 "
+                     "stands in for it",
+           "configs": {}}
+    for wl in [headline] + list(others):
+        p2, w2 = (per, what) if wl is headline else cpu_time_per_call(wl, seconds / 3, threads)
+        e = {"us_per_call": round(p2 * 1e6, 1), "sample": w2}
+        if wl.name.startswith("C4"):
+            e["GFLOPs"] = round(wl.flops() / p2 / 1e9, 1)
+        else:
+            e["GBps"] = round(wl.algorithmic_bytes() / p2 / 1e9, 3)
+        out["configs"][wl.name] = e
+    return out
 
 
 def copy_calibration(mib: int, iters: int):
@@ -240,7 +300,8 @@ def main():
     if extra:
         out["extra"] = extra
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(wl, [workloads.make(n) for n in ("C1", "C3", "C4", "C5")],
+                                           args.cpu_seconds)
     backend.Finalize()
     print(json.dumps(out), flush=True)
 
