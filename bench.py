@@ -240,6 +240,8 @@ def main():
     ap.add_argument("--extra", default="C3,C4,C5,G1,G2,R1,D1", help="comma list of other configs to report under 'extra'")
     ap.add_argument("--only", default="", help="run only this config (profiling passes); prints its entry")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-crossover", dest="crossover", action="store_false",
+                    help="skip the 32/64-row GEMM-vs-GEMV comparison")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--dot-table", action="store_true",
                     help="only time the reference's BenchmarkDotGeneral model shapes (f32 and bf16), one line each")
@@ -297,6 +299,18 @@ def main():
         w2 = workloads.make(name)
         steps = 100 if name == "C5" else max(3, min(args.steps, 50))
         extra[w2.name] = extra_entry(w2, measure(backend, w2, steps, 5))
+    if args.crossover:
+        # Rows 17..64 with per-channel int8: the GEMM (default plan) against the GEMV it replaced.
+        b2 = ca.New("mi355x,gemv_over_gemm")
+        for name in ("P32", "P64"):
+            w2 = workloads.make(name)
+            e = {}
+            for label, bk in (("gemm", backend), ("gemv", b2)):
+                r2 = measure(bk, w2, max(3, min(args.steps, 50)), 5)
+                e[label] = {"us_per_call": round(r2["ms_per_step"] * 1e3, 2), "kernel": r2["kernel"],
+                            "kernel_us_per_call": round(r2["kernel_us_per_step"], 3)}
+            extra[w2.name] = e
+        b2.Finalize()
     if extra:
         out["extra"] = extra
     if not args.no_cpu_baseline:

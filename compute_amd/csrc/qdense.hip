@@ -174,6 +174,9 @@ static QPath choose_path(const mx_backend* b, const QDenseDesc& d) {
   if (d.M == 0 || d.N == 0) return QPath::kEmpty;
   if (d.scheme == MX_QUANT_GGML || b->exact_qdense) return QPath::kExact;
   if (qdense_skinny_fits(d)) return QPath::kSkinny;
+  // Past the skinny kernel's 16 rows the GEMM reads every weight once, while the GEMV reads the
+  // whole weight matrix again for every 4 rows: the GEMV takes only what the GEMM does not fit.
+  if (!b->gemv_over_gemm && qdense_gemm_fits(d)) return QPath::kGemm;
   if (qdense_gemv_fits(d)) return QPath::kGemv;
   if (qdense_gemm_fits(d)) return QPath::kGemm;
   return QPath::kExact;

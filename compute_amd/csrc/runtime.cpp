@@ -292,7 +292,7 @@ int mx_backend_new(const char* config, mx_backend** out) {
   *out = nullptr;
   std::string cfg = config ? config : "";
   int device = 0;
-  bool host_only = false, no_fusion = false, exact = false;
+  bool host_only = false, no_fusion = false, exact = false, gemv_over_gemm = false;
   // Comma-separated options, mirroring the "name:cfg" convention of GOMLX_BACKEND (compute.go:141-147).
   size_t pos = 0;
   while (pos <= cfg.size()) {
@@ -304,6 +304,8 @@ int mx_backend_new(const char* config, mx_backend** out) {
       no_fusion = true;
     } else if (opt == "exact") {
       exact = true;
+    } else if (opt == "gemv_over_gemm") {
+      gemv_over_gemm = true;
     } else if (opt.rfind("device=", 0) == 0) {
       char* end = nullptr;
       long v = strtol(opt.c_str() + 7, &end, 10);
@@ -320,6 +322,7 @@ int mx_backend_new(const char* config, mx_backend** out) {
   b->host_only = host_only;
   b->no_fusion = no_fusion;
   b->exact_qdense = exact;
+  b->gemv_over_gemm = gemv_over_gemm;
   if (host_only) {
     b->description = "MI355X backend (host_only: graph building only)";
     *out = b;

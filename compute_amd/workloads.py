@@ -352,6 +352,13 @@ def make(name: str, seed: int = 0) -> QDWorkload:
             sc = bf16_from_f32(rs.uniform(0.002, 0.02, (K // G, N)).astype(np.float32))
             ws.append((w, sc, K, N))
         return MLPWorkload("C5_mlp_int4_g128_batch8", M, D, F, G, x, ws)
+    if name in ("P32", "P64"):  # small-batch prefill: int8 per-channel, bf16 x, the C2 matrix size
+        M, K, N = int(name[1:]), 4096, 11008
+        x = bf16_from_f32(rx.standard_normal((M, K)).astype(np.float32))
+        w = rw.integers(-127, 128, (K, N)).astype(np.int8)
+        s = rs.uniform(0.001, 0.01, N).astype(np.float32)
+        return QDWorkload(f"P{M}_int8_perchannel_bf16", M, K, N, BFloat16, Int8, Float32, (N,), 0, K, None, 0,
+                          x, w, s, None)
     if name == "D1":  # DotGeneral bf16 at the C4 (prefill) shape
         M, K, N = 2048, 4096, 4096
         x = bf16_from_f32(rx.standard_normal((M, K)).astype(np.float32))

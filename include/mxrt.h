@@ -153,7 +153,8 @@ typedef uint64_t mx_value;
  * only; every device operation then fails with MX_ERR_NO_DEVICE); "nofusion" (compile graphs op
  * by op); "exact" (FusedQuantizedDense always in the reference's loop order, bit-identical to
  * quantizeddense.go:586-650 at every size; without it, decode and prefill shapes take the fast
- * kernels, which differ only in summation order). */
+ * kernels, which differ only in summation order); "gemv_over_gemm" (measurement only: bf16 x with
+ * 17..64 rows takes the GEMV even where the prefill GEMM fits, which it otherwise prefers). */
 int mx_backend_new(const char* config, mx_backend** out);
 /* Backend.Finalize (compute.go:95). Frees all device memory; later calls fail MX_ERR_FINALIZED. */
 int mx_backend_finalize(mx_backend* b);

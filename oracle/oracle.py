@@ -100,6 +100,27 @@ def bf16_to_f32(h) -> np.ndarray:
     return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def rmsnorm_chain(x_bits: np.ndarray, eps: float, return_inv: bool = False):
+    """The MLP's RMSNorm as the reference executes its graph, op by op in f32 (bf16 x in, bf16 out):
+      xf = ConvertDType(x, F32); ms = ReduceSum(xf * xf, 1) * f32(1/D); inv = Rsqrt(ms + f32(eps));
+      h = ConvertDType(xf * inv, BF16).
+    ReduceSum adds the row's elements in order into an f32 accumulator starting at 0
+    (execReduceSumGeneric, internal/gobackend/ops/reduce.go:403-414); Rsqrt is
+    float32(1 / math.Sqrt(float64(v))) (execRsqrtGeneric, internal/gobackend/ops/unaryops.go:812-816);
+    every other op rounds its f32 result once.  return_inv also returns the f32 Rsqrt per row."""
+    xf = bf16_to_f32(x_bits).astype(np.float32)
+    M, D = xf.shape
+    sq = (xf * xf).astype(np.float32)
+    acc = np.zeros(M, dtype=np.float32)
+    for k in range(D):  # sequential over the row, vectorised over rows
+        acc = (acc + sq[:, k]).astype(np.float32)
+    ms = (acc * np.float32(1.0 / D)).astype(np.float32)
+    v = (ms + np.float32(eps)).astype(np.float32)
+    inv = (1.0 / np.sqrt(v.astype(np.float64))).astype(np.float32)
+    h = bf16_round((xf * inv[:, None]).astype(np.float32))
+    return (h, inv) if return_inv else h
+
+
 def unpack_int4(packed, signed=True) -> np.ndarray:
     p = np.ascontiguousarray(np.asarray(packed, dtype=np.uint8))
     out = np.empty(p.size * 2, dtype=np.int8)

@@ -305,6 +305,16 @@ def test_qdense_plan_selection():
                          block_size=4096) == want("qdense_gemv_i4")
             assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
                          block_size=4096) == want("qdense_gemm_mfma_i8")
+            # Past the skinny kernel's 16 rows, bf16 x with per-channel int8/uint8 takes the GEMM
+            # (weights read once) rather than the GEMV (weights re-read for every 4 rows).
+            for M in (17, 32, 64):
+                assert _plan(b, M, 4096, 11008, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
+                             block_size=4096) == want("qdense_gemm_mfma_i8")
+                assert _plan(b, M, 4096, 11008, x_dtype=BF16, w_dtype=ca.Uint8, s_dtype=BF16, block_axis=0,
+                             block_size=4096) == want("qdense_gemm_mfma_u8")
+            # Where the GEMM does not fit (K-grouped scales here), rows up to 64 stay on the GEMV.
+            assert _plan(b, 32, 4096, 11008, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
+                         block_size=64) == want("qdense_gemv_i8")
             # Small problems, M > 64 with the reference layout, unsupported block sizes: reference order.
             assert _plan(b, 1, 512, 1024, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=64) == "qdense_exact"
@@ -316,3 +326,11 @@ def test_qdense_plan_selection():
                          block_size=16) == "qdense_exact"
         finally:
             b.Finalize()
+    b = ca.New("host_only,gemv_over_gemm")
+    try:
+        assert _plan(b, 32, 4096, 11008, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
+                     block_size=4096) == "qdense_gemv_i8"
+        assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
+                     block_size=4096) == "qdense_gemm_mfma_i8"
+    finally:
+        b.Finalize()

@@ -58,3 +58,14 @@ def test_gemm_c4_config_full_size(backend):
     rows = np.sort(np.random.default_rng(4).choice(p.M, 128, replace=False))
     y = check_rows(r, rows=rows, threads=8, what="C4")
     assert np.array_equal(y, r.run())
+
+
+@pytest.mark.parametrize("M", [17, 32, 64])
+def test_gemm_small_batch_rows(backend, M):
+    """17..64 bf16 rows with per-channel int8 (the GEMV's row range): the GEMM takes them, at the
+    C2 matrix size, with the same bounds."""
+    p = O.make_problem(M, 4096, 11008, w_dtype=O.DT_INT8, block_axis=0, block_size=4096, per_channel_1d=True,
+                       scale_dtype=O.DT_FLOAT32, bias=False, seed=M)
+    r = QDenseRun(backend, p)
+    assert r.plan() == "qdense_gemm_mfma_i8"
+    check_rows(r, threads=8, what=f"M={M}")

@@ -1,6 +1,9 @@
 """The quantized MLP built through the Builder API and executed on the
 GPU, checked op by op against the CPU oracle on the GPU's own intermediate values:
-  - h = bf16(RMSNorm(x)) computed in f32: bit-exact against numpy (f64 mean, f32 scaling);
+  - h = bf16(RMSNorm(x)) computed in f32: within one bf16 ulp of the oracle's restatement of the
+    reference graph (sequential f32 ReduceSum, Rsqrt through f64; oracle.rmsnorm_chain, pinned by
+    closed forms in test_oracle).  The GPU adds each row's squares in another order (strided
+    partial sums and an LDS tree), so the f32 mean square may differ in its last bits;
   - gate = SiLU(FusedQuantizedDense(h)), up and down = FusedQuantizedDense(...): within the
     north star's rel 1e-2 / abs 1e-3 of the reference loop (the oracle) on the same inputs;
   - gate*up and the residual add: bit-exact bf16 products / sums of the GPU's operands.
@@ -54,8 +57,11 @@ def test_mlp_graph_c5(backend):
     bufs = wl.upload(backend)
     H, G, U, GU, D, Y = [o.ToFlatData().reshape(wl.M, -1) for o in build_instrumented(backend, wl).Execute(bufs)]
     x = O.bf16_to_f32(wl.x).astype(np.float32)
-    ms = (x.astype(np.float64) ** 2).mean(axis=1, keepdims=True)
-    assert np.array_equal(H, O.bf16_round((x / np.sqrt(ms + wl.eps)).astype(np.float32))), "RMSNorm"
+    h_ref = O.rmsnorm_chain(wl.x, wl.eps)
+    same_sign = (H >> 15) == (h_ref >> 15)
+    ulps = np.abs(H.astype(np.int32) - h_ref.astype(np.int32))  # adjacent bf16 values differ by 1
+    assert np.all(same_sign & (ulps <= 1)), "RMSNorm beyond one bf16 ulp"
+    assert np.mean(ulps == 0) > 0.99, "RMSNorm: more than 1% of elements off by an ulp"
     (wg, sg, K1, N1), (wu, su, _, _), (wd, sd, K3, N3) = wl.weights
     assert_bf16_close(G, qd_ref(wl, H, wg, sg, K1, N1, O.ACT_SILU), what="gate")
     assert_bf16_close(U, qd_ref(wl, H, wu, su, K1, N1, O.ACT_NONE), what="up")

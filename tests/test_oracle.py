@@ -297,3 +297,37 @@ def test_dot_general_kats():
     lhs = ((np.arange(np.prod(k["lhs_shape"])) + 1.0) * 1e-5).reshape(k["lhs_shape"])
     got = O.dot_general(lhs, [2], [], np.ones(k["rhs_shape"]), [0], [])
     assert abs(got[0, 0, 0] - k["want_out_0_0_0"]) < k["tolerance"]
+
+
+def test_rmsnorm_chain_closed_forms():
+    """Constant rows c: the sequential f32 sum of D squares is D c^2 exactly (multiples of c^2 with
+    few significant bits), so h = bf16(c / sqrt(c^2 + eps)); with eps = 0 that is exactly +-1.
+    Alternating signs give the same magnitudes; a row scaled by 2^k normalises to the same h."""
+    D = 4096
+    for c in (0.75, -1.5, 3.0):
+        x = O.bf16_round(np.full((2, D), c, np.float32))
+        h = O.rmsnorm_chain(x, 0.0)
+        assert np.all(O.bf16_to_f32(h) == np.sign(c)), c
+        alt = O.bf16_round(np.tile(np.array([c, -c], np.float32), (1, D // 2)))
+        assert np.array_equal(np.abs(O.bf16_to_f32(O.rmsnorm_chain(alt, 0.0))), np.ones((1, D), np.float32))
+        h_eps = O.bf16_to_f32(O.rmsnorm_chain(x, 1e-6))
+        want = np.float32(c) / np.sqrt(np.float64(c) ** 2 + np.float64(np.float32(1e-6)))
+        assert np.all(np.abs(h_eps - want) <= 2.0 ** -8 * abs(want)), c
+    rng = np.random.default_rng(3)
+    xf = rng.standard_normal((3, 512)).astype(np.float32)
+    a = O.rmsnorm_chain(O.bf16_round(xf), 0.0)
+    b = O.rmsnorm_chain(O.bf16_round(xf * 8.0), 0.0)
+    assert np.array_equal(a, b)
+
+
+def test_rmsnorm_chain_sum_is_sequential():
+    """A row whose in-order f32 sum differs from the exact sum: 4096^2 = 2^24 first, then 63 ones,
+    each of which is lost in f32 (2^24 + 1 rounds to 2^24).  In order the mean square is exactly
+    2^24 / 64 = 2^18 and Rsqrt is 2^-9; any order that adds the ones first gives another f32."""
+    D = 64
+    x = np.ones((1, D), np.float32)
+    x[0, 0] = 4096.0
+    _, inv = O.rmsnorm_chain(O.bf16_round(x), 0.0, return_inv=True)
+    assert inv[0] == np.float32(2.0 ** -9)
+    exact = 1.0 / np.sqrt((2.0 ** 24 + 63) / 64)
+    assert np.float32(exact) != np.float32(2.0 ** -9)
