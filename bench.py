@@ -198,7 +198,7 @@ def extra_entry(wl, r):
     nbytes = wl.algorithmic_bytes()
     e = {"us_per_call": round(r["ms_per_step"] * 1e3, 2), "kernel": r["kernel"], "kernel_us": round(r["kernel_us"], 3),
          "kernel_us_per_call": round(r["kernel_us_per_step"], 3)}
-    if wl.name.startswith("C4") or wl.name.startswith("D1"):
+    if wl.name.startswith("C4") or wl.name.startswith("D1") or wl.name.startswith("Q"):
         e["TFLOPs_kernel"] = round(wl.flops() / (r["kernel_us"] * 1e-6) / 1e12, 1)
         e["roofline"] = mfma_roofline(wl.flops(), r["kernel_us"], traffic_for(wl.name))
     elif wl.name.startswith("C5"):
@@ -237,7 +237,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--extra", default="C3,C4,C5,G1,G2,R1,D1", help="comma list of other configs to report under 'extra'")
+    ap.add_argument("--extra", default="C3,C4,C5,Q1,Q2,G1,G2,R1,D1", help="comma list of other configs to report under 'extra'")
     ap.add_argument("--only", default="", help="run only this config (profiling passes); prints its entry")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-crossover", dest="crossover", action="store_false",

@@ -186,7 +186,12 @@ static const char* path_name(const QDenseDesc& d, QPath p) {
   switch (p) {
     case QPath::kEmpty: return "empty";
     case QPath::kGemm:
-      return d.w_dt == MX_DTYPE_INT8 ? "qdense_gemm_mfma_i8" : "qdense_gemm_mfma_u8";
+      switch (d.w_dt) {
+        case MX_DTYPE_INT8: return d.block_size < d.K ? "qdense_gemm_mfma_i8_grouped" : "qdense_gemm_mfma_i8";
+        case MX_DTYPE_UINT8: return d.block_size < d.K ? "qdense_gemm_mfma_u8_grouped" : "qdense_gemm_mfma_u8";
+        case MX_DTYPE_INT4: return d.block_size < d.K ? "qdense_gemm_mfma_i4_grouped" : "qdense_gemm_mfma_i4";
+        default: return d.block_size < d.K ? "qdense_gemm_mfma_u4_grouped" : "qdense_gemm_mfma_u4";
+      }
     case QPath::kSkinny:
       switch (d.w_dt) {
         case MX_DTYPE_INT4: return "qdense_skinny_mfma_i4";

@@ -1,25 +1,31 @@
-// Prefill FusedQuantizedDense on gfx950: a bf16 MFMA GEMM with the int8 weights dequantised on
-// the fly, for M > 16 rows of bf16 activations and one scale per output column.
+// Prefill FusedQuantizedDense on gfx950: a bf16 MFMA GEMM with the Int8 / Uint8 / Int4 / Uint4
+// weights dequantised on the fly, for M > 16 rows of bf16 activations and one scale per output
+// column or per group of G rows (G a multiple of 64) and output column.
 //
 // Reference semantics: quantizedDenseLinearInt (internal/gobackend/fusedops/quantizeddense.go:
-// 616-650) then the activation epilogue (fusedops/dense.go:176-205).  With a per-channel scale
-// s[n] the reference's terms (x*w)*s factor as  y[m,n] = act(bias[n] + s[n] * sum_k x[m,k]*w[k,n]);
-// every product x*w is exact in f32, so only the summation order differs from the reference.
+// 616-650, the 4-bit unpack at :383-390) then the activation epilogue (fusedops/dense.go:176-205).
+// The reference's terms (x*w)*s factor per scale group:
+//   y[m,n] = act(bias[n] + sum_g s[g,n] * sum_{k in g} x[m,k]*w[k,n]),
+// with one group for per-channel scales; every product x*w is exact in f32 (bf16 x, |w| < 256),
+// so only the summation order differs from the reference.  With groups, the MFMAs of a group
+// accumulate into a second set of registers that is folded into the total with the group's
+// scales (acc += accg * s[g]) at the group's last block.
 //
 // Tiling.  A workgroup (8 waves, two per SIMD) computes a 256 x 128 output tile; wave w owns
 // rows [64 wr, 64 wr + 64) x columns [64 wc, 64 wc + 64) with wr = w % 4, wc = w / 4.  K advances
 // in blocks of 64 (two 32-row steps of v_mfma_f32_16x16x32_bf16).  LDS holds two buffers of
 //   - x: [256 rows][64 k] bf16; 16-byte k-chunks XOR-swizzled within each row by (row >> 1) & 7
 //     so that an MFMA operand read (16 rows) hits distinct banks;
-//   - Bt: [128 columns][64 k] bf16, the int8 weights converted exactly to bf16 (|w| < 256 has at
-//     most 8 significant bits) and transposed.  Column c is stored in row p = c ^ ((c >> 2) & 1)
+//   - Bt: [128 columns][64 k] bf16, the weights converted exactly to bf16 (|w| < 256 has at most
+//     8 significant bits) and transposed.  Column c is stored in row p = c ^ ((c >> 2) & 1)
 //     and its 16-byte k-chunks are XOR-swizzled by (p >> 3) & 7: the 16 lanes of a B-operand read
 //     (columns 4 apart) then cover both halves of the banks and 8 distinct chunks in each.
 // Block kb runs its MFMAs from buffer kb % 2 while the workgroup's loads of block kb + 4 travel
-// into registers (four blocks of lead cover an L2 miss) and block kb + 1, loaded three blocks
-// earlier, is written into the other buffer: each thread loads 4 x 16 bytes of x (8 threads per
-// 128-byte row segment) and 4 rows x 4 columns of int8 weights (32 threads per 128-byte row
-// segment) per block.  One barrier per block publishes the next buffers and retires the reads
+// into registers (four blocks of lead cover an L2 miss; two with scale groups, whose second
+// accumulator set takes the registers) and block kb + 1, loaded earlier, is written into the
+// other buffer: each thread loads 4 x 16 bytes of x (8 threads per 128-byte row segment) and
+// 4 rows x 4 columns of 8-bit weights (32 threads per 128-byte row segment) or 2 rows x 8
+// columns of 4-bit weights (16 threads per 64-byte row segment) per block.  One barrier per block publishes the next buffers and retires the reads
 // of the current ones; it sits between the block's two steps, so that the next block's step-0
 // operand reads travel under step 1's MFMAs.  Every access is compiler-visible (the compiler
 // places the waits), and sched_group_barrier interleaves the memory instructions one per MFMA:
@@ -52,14 +58,16 @@ constexpr int kLds = 2 * kABytes + 2 * kBtBytes;
 constexpr int kXLoads = kABytes / (kThreads * 16);  // 16-byte x loads per thread per block
 constexpr int kWLoads = 4;                           // w loads (4 bytes) per thread per block
 constexpr int kPf = 4;                               // blocks loaded ahead into registers
+constexpr int kPfGrouped = 2;                        // the same with scale groups
 constexpr int kUnroll = 4;                           // multiple of kPf and of the 2 LDS buffers
 static_assert(kXLoads * kThreads * 16 == kABytes, "x load split");
 static_assert(kBK * kBN == 16 * kThreads, "conversion: 16 weights per thread");
 
 // B operand kinds: the quantized weights [K, N] (int8 / uint8, converted to bf16), or a
 // DotGeneral right-hand side in bf16 / f16, [K, N] (transposed on the way into LDS) or [N, K].
-enum GemmB { kBI8 = 0, kBU8, kBBf16KN, kBF16KN, kBBf16NK, kBF16NK };
+enum GemmB { kBI8 = 0, kBU8, kBI4, kBU4, kBBf16KN, kBF16KN, kBBf16NK, kBF16NK };
 template <int BK> constexpr bool kDotB = BK >= kBBf16KN;
+template <int BK> constexpr bool k4B = BK == kBI4 || BK == kBU4;
 template <int BK> constexpr bool kF16B = BK == kBF16KN || BK == kBF16NK;
 template <int BK> constexpr bool kNKB = BK == kBBf16NK || BK == kBF16NK;
 
@@ -70,6 +78,7 @@ struct GemmArgs {
   const void* bias;   // [N] or null (quantized)
   void* out;          // [M, N] bf16 (quantized) or [batch][M, N] f32 / bf16 / f16 (DotGeneral)
   int M, K, N, s_dt, b_dt, act, tiles_n, grouped, tiles, out_dt;
+  int gpb;            // blocks of 64 K rows per scale group (grouped scales; scale is [K/G, N])
 };
 
 template <int BK>
@@ -124,8 +133,10 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
   }
 }
 
-template <int BK>
+template <int BK, bool GRP>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
+  constexpr int PF = GRP ? kPfGrouped : kPf;
+  static_assert(kUnroll % PF == 0, "register slots cycle within the unroll");
   // Tile order: consecutive work items go to one XCD (workgroups are dispatched round-robin over
   // the 8); with whole 2 x 16 tile groups, 32 consecutive items form one group.  DotGeneral
   // batches are consecutive runs of items.
@@ -184,12 +195,18 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // half type).  Columns past N read column 0 (their outputs are not stored).
   // [N, K] kinds: B rows are k-contiguous like x: thread t copies 16-byte chunks q = t + kThreads*i,
   // column q / 8 (rows past N read row N-1), k-chunk q % 8.
+  // 4-bit kinds: thread t converts columns 8*cq .. 8*cq + 7 and rows 2*j, 2*j + 1 of each block
+  // (cq = t % 16, j = t / 16); the 16 threads of a j read one 64-byte row segment.
   constexpr int kEB = kDotB<BK> ? 2 : 1;  // bytes per B element
-  const int cq = t & 31, j = t >> 5;
-  const int wcol = n0 + 4 * cq + 4 <= a.N ? n0 + 4 * cq : 0;
-  const uint8_t* wsrc = a.w + ((size_t)(4 * j) * N + wcol) * kEB;
+  const int cq = k4B<BK> ? (t & 15) : (t & 31), j = k4B<BK> ? (t >> 4) : (t >> 5);
+  const int cpt = k4B<BK> ? 8 : 4;  // columns per thread
+  const int wcol = n0 + cpt * cq + cpt <= a.N ? n0 + cpt * cq : 0;
+  const uint8_t* wsrc = k4B<BK> ? a.w + ((size_t)(2 * j) * N + wcol) / 2 : a.w + ((size_t)(4 * j) * N + wcol) * kEB;
   // Column 4*cq + c lives in Bt row (4*cq + c) ^ (cq & 1), k-chunk j / 2 swizzled by (cq / 2) & 7.
-  const uint32_t cv_off = (uint32_t)((((j >> 1) ^ ((cq >> 1) & 7)) << 4) + ((j & 1) << 3));
+  // 4-bit: column 8*cq + c in Bt row (8*cq + c) ^ ((c >> 2) & 1), k-chunk j / 4 swizzled by cq & 7,
+  // 4-byte pair (rows 2j, 2j + 1) j % 4 of the chunk.
+  const uint32_t cv_off = k4B<BK> ? (uint32_t)((((j >> 2) ^ (cq & 7)) << 4) + ((j & 3) << 2))
+                                  : (uint32_t)((((j >> 1) ^ ((cq >> 1) & 7)) << 4) + ((j & 1) << 3));
   constexpr int kNKLoads = kBtBytes / (kThreads * 16);
   const uint8_t* nksrc[kNKLoads];
   uint32_t nkdst[kNKLoads];
@@ -203,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     }
   }
   // Register words of one block of B per thread.
-  constexpr int kWWords = kNKB<BK> ? 4 * kNKLoads : (kDotB<BK> ? 2 * kWLoads : kWLoads);
+  constexpr int kWWords = kNKB<BK> ? 4 * kNKLoads : (kDotB<BK> ? 2 * kWLoads : (k4B<BK> ? 2 : kWLoads));
   auto load_w = [&](int kb, uint32_t (&dst)[kWWords]) {
     kb = min(kb, KB - 1);
     if constexpr (kNKB<BK>) {
@@ -220,6 +237,10 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
         dst[2 * e] = v[0];
         dst[2 * e + 1] = v[1];
       }
+    } else if constexpr (k4B<BK>) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        dst[e] = __builtin_nontemporal_load((const uint32_t*)(wsrc + (size_t)(kb * kBK + e) * (N / 2)));
     } else {
 #pragma unroll
       for (int e = 0; e < kWLoads; ++e)
@@ -229,7 +250,23 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // Four k-values of each of four consecutive columns (Bt rows 128 bytes apart): int8 converted
   // exactly to bf16, half values regrouped by column.  [N, K]: the chunks as loaded.
   auto store_w = [&](const uint32_t (&w4)[kWWords], int buf) {
-    if constexpr (kNKB<BK>) {
+    if constexpr (k4B<BK>) {
+      // Nibble c of each row word is column 8*cq + c (reference packing: low nibble first);
+      // both rows converted exactly through f32 and packed as a bf16 pair.
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float f[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          if constexpr (BK == kBI4)
+            f[e] = (float)((int32_t)(w4[e] << (28 - 4 * c)) >> 28);
+          else
+            f[e] = (float)((w4[e] >> (4 * c)) & 15u);
+        }
+        const uint32_t v = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
+        *(uint32_t*)(&bt[buf][cv_off + (uint32_t)((8 * cq + (c ^ ((c >> 2) & 1))) * (kBK * 2))]) = v;
+      }
+    } else if constexpr (kNKB<BK>) {
 #pragma unroll
       for (int i = 0; i < kNKLoads; ++i)
         *(u32x4_v*)(&bt[buf][nkdst[i]]) = u32x4_v{w4[4 * i], w4[4 * i + 1], w4[4 * i + 2], w4[4 * i + 3]};
@@ -259,11 +296,21 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     }
   };
 
-  f32x4_t acc[4][4];
+  // acc: the total; accg: the current scale group's sums (grouped scales only).
+  f32x4_t acc[4][4], accg[4][4];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < 4; ++c) acc[rb][c] = accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // Grouped scales: this lane's 4 columns' scales of the group being summed, loaded a group ahead.
+  const int scol = min(n0 + 64 * wc + 4 * cg, a.N - 4);
+  float sg[4] = {0.f, 0.f, 0.f, 0.f};
+  auto load_sg = [&](int g) __attribute__((always_inline)) {
+    g = min(g, a.K / (kBK * max(a.gpb, 1)) - 1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sg[c] = load_f(a.scale, (size_t)g * N + scol + c, a.s_dt);
+  };
+  if constexpr (GRP) load_sg(0);
 
   // MFMA operands of one 32-row step: x row 64*wr + 16*rb + cg, Bt column 64*wc + 4*cg + c (Bt
   // row 64*wc + 4*cg + (c ^ (cg & 1))).
@@ -280,11 +327,28 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) B[c] = *(const u32x4_v*)(bp + (c ^ b_par) * (kBK * 2));
   };
-  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[4]) {
+  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[rb][c] = mfma<BK>(A[rb], B[c], acc[rb][c]);
+      for (int c = 0; c < 4; ++c) {
+        if constexpr (GRP)
+          accg[rb][c] = mfma<BK>(A[rb], B[c], accg[rb][c]);
+        else
+          acc[rb][c] = mfma<BK>(A[rb], B[c], acc[rb][c]);
+      }
+  };
+  // End of scale group g: acc += accg * s[g] (column c of the lane), accg = 0, next group's scales.
+  auto fold = [&](int g) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[rb][c][r] = __builtin_fmaf(accg[rb][c][r], sg[c], acc[rb][c][r]);
+        accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    load_sg(g + 1);
   };
 
   // Register slots hold the next kPf blocks' x and w: block kb's slot is free once block kb
@@ -294,12 +358,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // step 1's reads and block kb + 1's writes are issued before step 0's MFMAs, and after the
   // barrier that publishes block kb + 1, its step-0 reads are issued before step 1's MFMAs.
   // (sched_barrier keeps the compiler from regrouping the phases.)
-  u32x4_v xr[kPf][kXLoads];
-  uint32_t wr4[kPf][kWWords];
+  u32x4_v xr[PF][kXLoads];
+  uint32_t wr4[PF][kWWords];
   u32x4_v A0[4], B0[4], A1[4], B1[4];
-  auto block = [&](int kb, auto step) {
+  auto block = [&](int kb, auto step) __attribute__((always_inline)) {
     constexpr int U = decltype(step)::value;  // kb % kUnroll
-    constexpr int S = U % kPf, S1 = (U + 1) % kPf, B = U % 2;
+    constexpr int S = U % PF, S1 = (U + 1) % PF, B = U % 2;
     // Step 0: its MFMAs interleaved with step 1's operand reads, then with the conversion and
     // LDS writes of block kb + 1, so that every issue stall of a memory instruction overlaps an
     // MFMA in flight.
@@ -323,8 +387,8 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     // Step 1: its MFMAs interleaved with block kb + 1's step-0 reads and the global loads of
     // block kb + kPf.
     read_step(B ^ 1, 0, A0, B0);
-    load_x(kb + kPf, xr[S]);
-    load_w(kb + kPf, wr4[S]);
+    load_x(kb + PF, xr[S]);
+    load_w(kb + PF, wr4[S]);
     mma_step(A1, B1);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -337,11 +401,14 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (GRP) {
+      if ((kb + 1) % a.gpb == 0) fold(kb / a.gpb);
+    }
   };
   auto blocks = [&](int kb, int n, auto... steps) { ((steps.value < n ? block(kb + steps.value, steps) : void()), ...); };
 
 #pragma unroll
-  for (int p = 0; p < kPf; ++p) {
+  for (int p = 0; p < PF; ++p) {
     load_x(p, xr[p]);
     load_w(p, wr4[p]);
   }
@@ -386,7 +453,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   float sc[4], bi[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    sc[c] = load_f(a.scale, ncol + c, a.s_dt);
+    sc[c] = GRP ? 1.0f : load_f(a.scale, ncol + c, a.s_dt);  // grouped: applied by fold()
     bi[c] = a.bias ? load_f(a.bias, ncol + c, a.b_dt) : 0.0f;
   }
   const int row0 = m0 + 64 * wr + 4 * kq;
@@ -407,10 +474,13 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 bool qdense_gemm_fits(const QDenseDesc& d) {
   auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
   const bool per_channel = d.block_axis == 0 && d.block_size >= d.K;
-  return d.M > 16 && d.x_dt == MX_DTYPE_BFLOAT16 && d.scheme == MX_QUANT_LINEAR && !d.zp && per_channel &&
-         (d.w_dt == MX_DTYPE_INT8 || d.w_dt == MX_DTYPE_UINT8) && d.K >= kBK && d.K % kBK == 0 && d.N >= 16 &&
-         d.N % 16 == 0 && d.M < (1 << 30) && d.K < (1 << 30) && d.N < (1 << 30) && aligned(d.w, 16) &&
-         aligned(d.x, 16) && aligned(d.out, 16);
+  // Scale groups of whole 64-row blocks that tile K exactly.
+  const bool grouped = d.block_axis == 0 && d.block_size < d.K && d.block_size % kBK == 0 && d.K % d.block_size == 0;
+  const bool wt = d.w_dt == MX_DTYPE_INT8 || d.w_dt == MX_DTYPE_UINT8 || d.w_dt == MX_DTYPE_INT4 ||
+                  d.w_dt == MX_DTYPE_UINT4;
+  return d.M > 16 && d.x_dt == MX_DTYPE_BFLOAT16 && d.scheme == MX_QUANT_LINEAR && !d.zp && (per_channel || grouped) &&
+         wt && d.K >= kBK && d.K % kBK == 0 && d.N >= 16 && d.N % 16 == 0 && d.M < (1 << 30) && d.K < (1 << 30) &&
+         d.N < (1 << 30) && aligned(d.w, 16) && aligned(d.x, 16) && aligned(d.out, 16);
 }
 
 int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
@@ -432,13 +502,29 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.tiles_n = (int)tiles_n;
   ga.grouped = (tiles_m % 2 == 0 && tiles_n % 16 == 0) ? 1 : 0;
   ga.tiles = (int)(tiles_m * tiles_n);
+  const bool grouped = d.block_size < d.K;
+  ga.gpb = grouped ? (int)(d.block_size / kBK) : 0;
   const int grid = (int)(tiles_m * tiles_n);
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
-    if (d.w_dt == MX_DTYPE_INT8)
-      dispatch(qdense_gemm_kernel<kBI8>, grid, kThreads, 0, st, ga);
-    else
-      dispatch(qdense_gemm_kernel<kBU8>, grid, kThreads, 0, st, ga);
+    switch (d.w_dt) {
+      case MX_DTYPE_INT8:
+        grouped ? dispatch(qdense_gemm_kernel<kBI8, true>, grid, kThreads, 0, st, ga)
+                : dispatch(qdense_gemm_kernel<kBI8, false>, grid, kThreads, 0, st, ga);
+        break;
+      case MX_DTYPE_UINT8:
+        grouped ? dispatch(qdense_gemm_kernel<kBU8, true>, grid, kThreads, 0, st, ga)
+                : dispatch(qdense_gemm_kernel<kBU8, false>, grid, kThreads, 0, st, ga);
+        break;
+      case MX_DTYPE_INT4:
+        grouped ? dispatch(qdense_gemm_kernel<kBI4, true>, grid, kThreads, 0, st, ga)
+                : dispatch(qdense_gemm_kernel<kBI4, false>, grid, kThreads, 0, st, ga);
+        break;
+      default:
+        grouped ? dispatch(qdense_gemm_kernel<kBU4, true>, grid, kThreads, 0, st, ga)
+                : dispatch(qdense_gemm_kernel<kBU4, false>, grid, kThreads, 0, st, ga);
+        break;
+    }
   });
 }
 
@@ -475,14 +561,14 @@ int dot_mfma_run(mx_backend* b, const DotDesc& d, const char* name) {
   return launch(b, name, [&] {
     if (d.rhs_transposed) {
       if (f16)
-        dispatch(qdense_gemm_kernel<kBF16NK>, grid, kThreads, 0, st, ga);
+        dispatch(qdense_gemm_kernel<kBF16NK, false>, grid, kThreads, 0, st, ga);
       else
-        dispatch(qdense_gemm_kernel<kBBf16NK>, grid, kThreads, 0, st, ga);
+        dispatch(qdense_gemm_kernel<kBBf16NK, false>, grid, kThreads, 0, st, ga);
     } else {
       if (f16)
-        dispatch(qdense_gemm_kernel<kBF16KN>, grid, kThreads, 0, st, ga);
+        dispatch(qdense_gemm_kernel<kBF16KN, false>, grid, kThreads, 0, st, ga);
       else
-        dispatch(qdense_gemm_kernel<kBBf16KN>, grid, kThreads, 0, st, ga);
+        dispatch(qdense_gemm_kernel<kBBf16KN, false>, grid, kThreads, 0, st, ga);
     }
   });
 }

@@ -359,6 +359,16 @@ def make(name: str, seed: int = 0) -> QDWorkload:
         s = rs.uniform(0.001, 0.01, N).astype(np.float32)
         return QDWorkload(f"P{M}_int8_perchannel_bf16", M, K, N, BFloat16, Int8, Float32, (N,), 0, K, None, 0,
                           x, w, s, None)
+    if name in ("Q1", "Q2"):  # prefill with K-grouped scales: Int4 g128 (the MLP's gate/up) / int8 g64
+        M, K, N = 2048, 4096, 14336
+        i4 = name == "Q1"
+        G = 128 if i4 else 64
+        x = bf16_from_f32(rx.standard_normal((M, K)).astype(np.float32))
+        w = pack_int4(rw.integers(-8, 8, K * N)) if i4 else rw.integers(-127, 128, (K, N)).astype(np.int8)
+        s = bf16_from_f32(rs.uniform(0.002, 0.02, (K // G, N)).astype(np.float32))
+        label = "Q1_prefill_int4_g128" if i4 else "Q2_prefill_int8_g64"
+        return QDWorkload(label, M, K, N, BFloat16, Int4 if i4 else Int8, BFloat16, (K // G, N), 0, G, None, 0,
+                          x, w, s, None)
     if name == "D1":  # DotGeneral bf16 at the C4 (prefill) shape
         M, K, N = 2048, 4096, 4096
         x = bf16_from_f32(rx.standard_normal((M, K)).astype(np.float32))

@@ -312,9 +312,19 @@ def test_qdense_plan_selection():
                              block_size=4096) == want("qdense_gemm_mfma_i8")
                 assert _plan(b, M, 4096, 11008, x_dtype=BF16, w_dtype=ca.Uint8, s_dtype=BF16, block_axis=0,
                              block_size=4096) == want("qdense_gemm_mfma_u8")
-            # Where the GEMM does not fit (K-grouped scales here), rows up to 64 stay on the GEMV.
-            assert _plan(b, 32, 4096, 11008, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
+            # Where the GEMM does not fit (f32 x here), rows up to 64 stay on the GEMV.
+            assert _plan(b, 32, 4096, 11008, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
                          block_size=64) == want("qdense_gemv_i8")
+            # Prefill with 4-bit weights and K-grouped scales: the GEMM with a scale-group fold.
+            assert _plan(b, 2048, 4096, 14336, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
+                         block_size=128) == want("qdense_gemm_mfma_i4_grouped")
+            assert _plan(b, 512, 4096, 4096, x_dtype=BF16, w_dtype=ca.Uint4, s_dtype=F32, block_axis=0,
+                         block_size=4096) == want("qdense_gemm_mfma_u4")
+            assert _plan(b, 2048, 4096, 14336, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=BF16, block_axis=0,
+                         block_size=64) == want("qdense_gemm_mfma_i8_grouped")
+            # Groups that do not tile K in 64-row blocks stay on the reference-order kernel.
+            assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
+                         block_size=96) == "qdense_exact"
             # Small problems, M > 64 with the reference layout, unsupported block sizes: reference order.
             assert _plan(b, 1, 512, 1024, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=64) == "qdense_exact"

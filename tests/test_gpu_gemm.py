@@ -69,3 +69,53 @@ def test_gemm_small_batch_rows(backend, M):
     r = QDenseRun(backend, p)
     assert r.plan() == "qdense_gemm_mfma_i8"
     check_rows(r, threads=8, what=f"M={M}")
+
+
+# ---------------------------------------------------------------------------------------------
+# 4-bit weights and K-grouped scales (scale [K/G, N], G a multiple of 64): the same GEMM with the
+# nibbles converted into the LDS tile and a per-group accumulator folded with the group's scales.
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("w_dtype", [O.DT_INT4, O.DT_UINT4, O.DT_INT8, O.DT_UINT8])
+@pytest.mark.parametrize("G", [None, 64, 128, 256])
+def test_gemm_4bit_and_groups(backend, w_dtype, G):
+    M, K, N = 300, 512, 272
+    p = O.make_problem(M, K, N, w_dtype=w_dtype, block_axis=0, block_size=G if G else K, per_channel_1d=G is None,
+                       scale_dtype=O.DT_BFLOAT16 if G else O.DT_FLOAT32, bias=True, seed=7 + (G or 0))
+    r = QDenseRun(backend, p)
+    want = "qdense_gemm_mfma_" + {O.DT_INT4: "i4", O.DT_UINT4: "u4", O.DT_INT8: "i8", O.DT_UINT8: "u8"}[w_dtype]
+    assert r.plan() == want + ("_grouped" if G else "")
+    check_rows(r, what=f"{w_dtype} G={G}")
+    assert np.array_equal(r.run(), r.run())
+
+
+@pytest.mark.parametrize("shape", [(17, 128, 16, 64), (1000, 1024, 4112, 128), (513, 2048, 1040, 512)])
+def test_gemm_grouped_shapes(backend, shape):
+    M, K, N, G = shape
+    p = O.make_problem(M, K, N, w_dtype=O.DT_INT4, block_axis=0, block_size=G, scale_dtype=O.DT_FLOAT32,
+                       bias=False, act=O.ACT_NONE, scale_range=(0.002, 0.02), seed=M)
+    r = QDenseRun(backend, p)
+    assert r.plan() == "qdense_gemm_mfma_i4_grouped"
+    check_rows(r, threads=8, what=f"{shape}")
+
+
+@pytest.mark.parametrize("act", [O.ACT_SILU, O.ACT_GELU])
+def test_gemm_grouped_activations(backend, act):
+    p = O.make_problem(64, 256, 256, w_dtype=O.DT_UINT4, block_axis=0, block_size=64, bias=True, act=act,
+                       scale_range=(0.01, 0.05), seed=act)
+    r = QDenseRun(backend, p)
+    assert r.plan() == "qdense_gemm_mfma_u4_grouped"
+    check_rows(r, what=f"act {act}")
+
+
+@pytest.mark.parametrize("w_dtype,G", [(O.DT_INT4, 128), (O.DT_INT8, 64)])
+def test_gemm_grouped_prefill_full_size(backend, w_dtype, G):
+    """x bf16 [2048,4096] x Int4 [4096,14336] g128 (the MLP's gate/up weights at prefill) and the
+    int8 g64 layout of BASELINE configs[2] at the same size: 128 seeded rows against the oracle,
+    two calls bit-equal."""
+    p = O.make_problem(2048, 4096, 14336, w_dtype=w_dtype, block_axis=0, block_size=G, bias=False,
+                       scale_range=(0.002, 0.02), seed=G)
+    r = QDenseRun(backend, p)
+    assert r.plan().endswith("_grouped")
+    rows = np.sort(np.random.default_rng(5).choice(p.M, 128, replace=False))
+    y = check_rows(r, rows=rows, threads=8, what=f"{w_dtype} g{G}")
+    assert np.array_equal(y, r.run())
