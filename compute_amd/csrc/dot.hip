@@ -4,10 +4,16 @@
 // [B,N,K] "Transposed" layouts, half-precision inputs accumulating into f32).
 //
 // The tiled kernel stages 64x64 output tiles through LDS, 16-deep in K, each thread owning a
-// 4x4 register block; it serves f64, small or unaligned f32 (accumulating in the input type)
-// and small bf16/f16 (accumulating in f32).  Larger contractions run on the matrix cores: the
+// 4x4 register block; it serves f64, small or unaligned f32 (accumulating in the input type),
+// small bf16/f16 (accumulating in f32) and the integer dtypes.  Integers accumulate modulo 2^32
+// (2^64 for 64-bit types) in an unsigned register and are stored truncated to the dtype: the low
+// bits of a modular sum of modular products are those of Go's wrapping arithmetic in the dtype
+// itself (the reference's noSIMD kernels, internal/gobackend/dot/matmul/nosimd.go:66-75), in
+// any summation order.  Larger contractions run on the matrix cores: the
 // small-tile dot_mm_kernel / dot_mm_lds_kernel below (f32, and half problems too small for
 // qdense_gemm.hip's 256x128-tile kernel), or that kernel.
+
+#include <type_traits>
 
 #include "device_common.h"
 #include "mxrt_internal.h"
@@ -19,7 +25,7 @@ constexpr int kDotKStep = 16;
 
 template <typename TI, typename TA>
 __device__ __forceinline__ TA load_acc(const TI* p, int64_t i, int dt) {
-  if constexpr (sizeof(TI) == 2) {
+  if constexpr (sizeof(TI) == 2 && std::is_floating_point<TA>::value) {  // bf16 / f16 storage
     const uint16_t h = ((const uint16_t*)p)[i];
     return (TA)(dt == MX_DTYPE_BFLOAT16 ? bf16_to_f32(h) : f16_to_f32(h));
   } else {
@@ -27,9 +33,9 @@ __device__ __forceinline__ TA load_acc(const TI* p, int64_t i, int dt) {
   }
 }
 
-template <typename TI, typename TA>
+template <typename TI, typename TA, typename TO = TA>
 __global__ __launch_bounds__(256) void dot_tiled_kernel(const TI* __restrict__ lhs, const TI* __restrict__ rhs,
-                                                        TA* __restrict__ out, int64_t M, int64_t K, int64_t N,
+                                                        TO* __restrict__ out, int64_t M, int64_t K, int64_t N,
                                                         bool rhs_t, int in_dt) {
   __shared__ TA As[kDotKStep][kDotTile + 1];
   __shared__ TA Bs[kDotKStep][kDotTile + 1];
@@ -79,7 +85,7 @@ __global__ __launch_bounds__(256) void dot_tiled_kernel(const TI* __restrict__ l
     }
     __syncthreads();
   }
-  TA* O = out + b * M * N;
+  TO* O = out + b * M * N;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t m = m0 + ty * 4 + i;
@@ -87,7 +93,7 @@ __global__ __launch_bounds__(256) void dot_tiled_kernel(const TI* __restrict__ l
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t n = n0 + tx * 4 + j;
-      if (n < N) O[m * N + n] = acc[i][j];
+      if (n < N) O[m * N + n] = (TO)acc[i][j];
     }
   }
 }
@@ -555,6 +561,30 @@ int dot_run(mx_backend* b, const DotDesc& d) {
         dispatch(dot_tiled_kernel<uint16_t, float>, grid, 256, 0, st, (const uint16_t*)d.lhs, (const uint16_t*)d.rhs,
                                                                  (float*)d.out, d.M, d.K, d.N, d.rhs_transposed, d.in_dt);
       });
+    default:
+      break;
+  }
+  // Integers: the output dtype is the input's (the graph converts to the accumulator dtype first).
+  auto int_dot = [&](auto ti, auto ta, const char* name) {
+    using TI = decltype(ti);
+    using TA = decltype(ta);
+    return launch(b, name, [&] {
+      dispatch(dot_tiled_kernel<TI, TA, TI>, grid, 256, 0, st, (const TI*)d.lhs, (const TI*)d.rhs, (TI*)d.out, d.M, d.K,
+               d.N, d.rhs_transposed, d.in_dt);
+    });
+  };
+  if (d.out_dt != d.in_dt)
+    return set_error(MX_ERR_NOT_IMPLEMENTED, "DotGeneral: %s inputs with %s output", dtype_name(d.in_dt),
+                     dtype_name(d.out_dt));
+  switch (d.in_dt) {
+    case MX_DTYPE_INT8: return int_dot(int8_t{}, uint32_t{}, "dot_tiled_i8");
+    case MX_DTYPE_UINT8: return int_dot(uint8_t{}, uint32_t{}, "dot_tiled_u8");
+    case MX_DTYPE_INT16: return int_dot(int16_t{}, uint32_t{}, "dot_tiled_i16");
+    case MX_DTYPE_UINT16: return int_dot(uint16_t{}, uint32_t{}, "dot_tiled_u16");
+    case MX_DTYPE_INT32: return int_dot(int32_t{}, uint32_t{}, "dot_tiled_i32");
+    case MX_DTYPE_UINT32: return int_dot(uint32_t{}, uint32_t{}, "dot_tiled_u32");
+    case MX_DTYPE_INT64: return int_dot(int64_t{}, uint64_t{}, "dot_tiled_i64");
+    case MX_DTYPE_UINT64: return int_dot(uint64_t{}, uint64_t{}, "dot_tiled_u64");
     default:
       return set_error(MX_ERR_NOT_IMPLEMENTED, "DotGeneral: dtype %s not implemented", dtype_name(d.in_dt));
   }

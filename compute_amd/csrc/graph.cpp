@@ -636,11 +636,14 @@ static int dot_general_idx(mx_function* fn, int lhs, const int32_t* lc, int n_lc
                        (long long)ls.dims[lb[i]], rb[i], (long long)rs.dims[rb[i]]);
   }
   const int in_dt = ls.dtype;
-  if (!dtype_is_float(in_dt))
-    return set_error(MX_ERR_NOT_IMPLEMENTED, "%s: dtype %s not implemented (float dtypes only)", op, dtype_name(in_dt));
-  if (acc_dt != MX_DTYPE_INVALID && !dtype_is_float(acc_dt))
+  // Float and (unpacked) integer dtypes, like the reference's registered implementations
+  // (dot/matmul/nosimd.go:66-75 for the integers); integer sums wrap in the accumulator dtype.
+  auto dot_dtype = [](int dt) { return dtype_is_float(dt) || (dtype_is_int(dt) && !dtype_is_packed(dt)); };
+  if (!dot_dtype(in_dt))
+    return set_error(MX_ERR_NOT_IMPLEMENTED, "%s: dtype %s not implemented", op, dtype_name(in_dt));
+  if (acc_dt != MX_DTYPE_INVALID && !dot_dtype(acc_dt))
     return set_error(MX_ERR_NOT_IMPLEMENTED, "%s: accumulator dtype %s not implemented", op, dtype_name(acc_dt));
-  if (out_dt != MX_DTYPE_INVALID && !dtype_is_float(out_dt))
+  if (out_dt != MX_DTYPE_INVALID && !dot_dtype(out_dt))
     return set_error(MX_ERR_NOT_IMPLEMENTED, "%s: output dtype %s not implemented", op, dtype_name(out_dt));
   const int final_dt = out_dt != MX_DTYPE_INVALID ? out_dt : in_dt;
 

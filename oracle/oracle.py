@@ -321,6 +321,43 @@ def dot_general(lhs: np.ndarray, lc, lb, rhs: np.ndarray, rc, rb) -> np.ndarray:
     return out.reshape(bshape + mshape + nshape)
 
 
+def dot_general_int(lhs: np.ndarray, lc, lb, rhs: np.ndarray, rc, rb, acc_dtype=None) -> np.ndarray:
+    """Integer DotGeneral as the reference computes it: inputs converted to the accumulator dtype
+    when one is given (convertToAccumulatorDType, internal/gobackend/dot/dot.go:340-372), products
+    and sums wrapping in that dtype (the noSIMD kernels' Go integer arithmetic,
+    dot/matmul/nosimd.go:66-75).  Brute force, one output element at a time, for small cases:
+    every product and partial sum is reduced modulo 2^bits and reinterpreted in the dtype."""
+    dt = np.dtype(acc_dtype) if acc_dtype is not None else lhs.dtype
+    bits = dt.itemsize * 8
+    mod = 1 << bits
+
+    def wrap(v: int) -> int:
+        v %= mod
+        return v - mod if (dt.kind == "i" and v >= mod // 2) else v
+
+    lc, lb, rc, rb = list(lc), list(lb), list(rc), list(rb)
+    lcross = [a for a in range(lhs.ndim) if a not in lc and a not in lb]
+    rcross = [a for a in range(rhs.ndim) if a not in rc and a not in rb]
+    L = np.transpose(lhs, lb + lcross + lc)
+    R = np.transpose(rhs, rb + rc + rcross)
+    bshape = [lhs.shape[a] for a in lb]
+    mshape = [lhs.shape[a] for a in lcross]
+    nshape = [rhs.shape[a] for a in rcross]
+    Bn, Mn, Nn = (int(np.prod(x, dtype=np.int64)) for x in (bshape, mshape, nshape))
+    Kn = int(np.prod([lhs.shape[a] for a in lc], dtype=np.int64))
+    L = L.reshape(Bn, Mn, Kn)
+    R = R.reshape(Bn, Kn, Nn)
+    out = np.zeros((Bn, Mn, Nn), dtype=dt)
+    for b in range(Bn):
+        for m in range(Mn):
+            for n in range(Nn):
+                acc = 0
+                for k in range(Kn):
+                    acc = wrap(acc + wrap(wrap(int(L[b, m, k])) * wrap(int(R[b, k, n]))))
+                out[b, m, n] = acc
+    return out.reshape(bshape + mshape + nshape)
+
+
 # ---------------------------------------------------------------------------------------------
 # GGML block formats (quantizeddense_ggml.go, quantizeddense.go:455-499).
 # ---------------------------------------------------------------------------------------------

@@ -365,3 +365,59 @@ def test_slice_exact(backend, strides):
     st = strides or [1, 1, 1, 1]
     want = x[tuple(slice(a, b, c) for a, b, c in zip(starts, limits, st))]
     assert np.array_equal(y, want)
+
+
+# ---------------------------------------------------------------------------------------------
+# Integer DotGeneral (the reference's noSIMD integer kernels, internal/gobackend/dot/matmul/
+# nosimd.go:66-75, after convertToAccumulatorDType, dot/dot.go:340-372): exact, with the sums
+# wrapping in the accumulator dtype, against the brute-force restatement oracle.dot_general_int.
+# ---------------------------------------------------------------------------------------------
+INT_CASES = [
+    # (input dtype, numpy dtype, accumulator, output, value range)
+    (ca.Int8, np.int8, None, None, (-128, 128)),          # wraps in int8
+    (ca.Int8, np.int8, ca.Int32, ca.Int32, (-128, 128)),
+    (ca.Int8, np.int8, ca.Int32, None, (-128, 128)),      # int32 sums converted back to int8
+    (ca.Int16, np.int16, None, None, (-30000, 30000)),
+    (ca.Int32, np.int32, None, None, (-(1 << 31), 1 << 31)),  # wraps in int32
+    (ca.Int64, np.int64, None, None, (-(1 << 62), 1 << 62)),  # wraps in int64
+    (ca.Uint8, np.uint8, None, None, (0, 256)),
+    (ca.Uint8, np.uint8, ca.Uint32, ca.Uint32, (0, 256)),
+    (ca.Uint32, np.uint32, None, None, (0, 1 << 32)),
+    (ca.Uint64, np.uint64, None, None, (0, 1 << 63)),
+]
+NP_OF = {ca.Int8: np.int8, ca.Int16: np.int16, ca.Int32: np.int32, ca.Int64: np.int64, ca.Uint8: np.uint8,
+         ca.Uint16: np.uint16, ca.Uint32: np.uint32, ca.Uint64: np.uint64}
+
+
+@pytest.mark.parametrize("case", INT_CASES, ids=lambda c: f"{c[0].name}-acc{c[2].name if c[2] else 'none'}-out{c[3].name if c[3] else 'none'}")
+@pytest.mark.parametrize("layout", ["plain", "transposed", "batched"])
+def test_integer_dot_general_exact(backend, case, layout):
+    dt, npdt, acc, out_dt, (lo, hi) = case
+    rng = np.random.default_rng(abs(hash((dt.name, layout))) % 1000)
+    if layout == "plain":      # [M, K] x [K, N]
+        ls, rs, lc, lb, rc, rb = (5, 7), (7, 3), [1], [], [0], []
+    elif layout == "transposed":  # [M, K] x [N, K]
+        ls, rs, lc, lb, rc, rb = (4, 9), (6, 9), [1], [], [1], []
+    else:                      # [K, B, M] x [B, N, K]
+        ls, rs, lc, lb, rc, rb = (6, 2, 3), (2, 4, 6), [0], [1], [2], [0]
+    l = rng.integers(lo, hi, ls, dtype=np.int64 if npdt != np.uint64 else np.uint64).astype(npdt)
+    r = rng.integers(lo, hi, rs, dtype=np.int64 if npdt != np.uint64 else np.uint64).astype(npdt)
+    got, gdt = run(backend, [(l, dt), (r, dt)],
+                   lambda f, p: f.DotGeneral(p[0], lc, lb, p[1], rc, rb,
+                                             ca.DotGeneralConfig(AccumulatorDType=acc or ca.InvalidDType,
+                                                                 OutputDType=out_dt or ca.InvalidDType)))
+    acc_np = NP_OF[acc] if acc is not None else None
+    want = O.dot_general_int(l, lc, lb, r, rc, rb, acc_dtype=acc_np)
+    final = out_dt if out_dt is not None else dt
+    assert gdt == final
+    assert np.array_equal(got, want.astype(NP_OF[final])), f"{case} {layout}"
+
+
+def test_integer_dot_general_large_int32(backend):
+    """A larger int32 contraction with no overflow: equal to the float64 matmul."""
+    rng = np.random.default_rng(11)
+    l = rng.integers(-100, 100, (2, 64, 128)).astype(np.int32)
+    r = rng.integers(-100, 100, (2, 128, 96)).astype(np.int32)
+    got, gdt = run(backend, [(l, ca.Int32), (r, ca.Int32)], lambda f, p: f.DotGeneral(p[0], [2], [0], p[1], [1], [0]))
+    assert gdt == ca.Int32
+    assert np.array_equal(got, np.matmul(l.astype(np.float64), r.astype(np.float64)).astype(np.int32))

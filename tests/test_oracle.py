@@ -331,3 +331,24 @@ def test_rmsnorm_chain_sum_is_sequential():
     assert inv[0] == np.float32(2.0 ** -9)
     exact = 1.0 / np.sqrt((2.0 ** 24 + 63) / 64)
     assert np.float32(exact) != np.float32(2.0 ** -9)
+
+
+def test_dot_general_int_closed_forms():
+    """Integer DotGeneral restatement: identity contraction, the int8 wrap (100 * 2 + 100 * 2 =
+    400 = -112 mod 256), int32 overflow (2^30 * 4 = 0 mod 2^32), an accumulator dtype that
+    avoids the wrap, unsigned wrap, and agreement with float64 matmul where nothing wraps."""
+    eye = np.eye(3, dtype=np.int32)
+    x = np.arange(6, dtype=np.int32).reshape(2, 3)
+    assert np.array_equal(O.dot_general_int(x, [1], [], eye, [0], []), x)
+    a = np.array([[100, 100]], np.int8)
+    b = np.array([[2], [2]], np.int8)
+    assert O.dot_general_int(a, [1], [], b, [0], [])[0, 0] == np.int8(-112)
+    assert O.dot_general_int(a, [1], [], b, [0], [], acc_dtype=np.int32)[0, 0] == 400
+    big = np.array([[1 << 30]], np.int32)
+    assert O.dot_general_int(big, [1], [], np.array([[4]], np.int32), [0], [])[0, 0] == 0
+    u = np.array([[255, 255]], np.uint8)
+    assert O.dot_general_int(u, [1], [], np.array([[255], [1]], np.uint8), [0], [])[0, 0] == (255 * 255 + 255) % 256
+    rng = np.random.default_rng(0)
+    l = rng.integers(-50, 50, (2, 3, 4)).astype(np.int32)
+    r = rng.integers(-50, 50, (2, 4, 5)).astype(np.int32)
+    assert np.array_equal(O.dot_general_int(l, [2], [0], r, [1], [0]), O.dot_general(l, [2], [0], r, [1], [0]).astype(np.int32))
