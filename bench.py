@@ -36,6 +36,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3
 MALL_BYTES = 256 << 20
 METRIC = "QuantizedDense GB/s & TFLOP/s vs MI355X roofline; µs/call at decode+prefill"
 
@@ -89,10 +90,11 @@ def hbm_roofline(nbytes: float, us: float, traffic):
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
 
 
-def mfma_roofline(flops: float, us: float, traffic):
+def mfma_roofline(flops: float, us: float, traffic, peak: float = None):
+    peak = peak or BF16_PEAK_TFLOPS
     achieved = flops / (us * 1e-6) / 1e12
-    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic}
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
 def _cpu_model() -> str:
@@ -201,6 +203,13 @@ def extra_entry(wl, r):
     if wl.name.startswith("C4") or wl.name.startswith("D1") or wl.name.startswith("Q"):
         e["TFLOPs_kernel"] = round(wl.flops() / (r["kernel_us"] * 1e-6) / 1e12, 1)
         e["roofline"] = mfma_roofline(wl.flops(), r["kernel_us"], traffic_for(wl.name))
+    elif wl.name.startswith("R3"):
+        # f32 x: the dequantised weights are contracted on the f32 matrix cores; the whole call
+        # (dequantisation, contraction, epilogue) priced against the dense f32 MFMA peak.
+        e["TFLOPs_call"] = round(wl.flops() / (r["kernel_us_per_step"] * 1e-6) / 1e12, 1)
+        e["kernels"] = {k: {"per_call": round(v["launches_per_step"], 2), "avg_us": round(v["avg_us"], 3)}
+                        for k, v in r["kernels"].items()}
+        e["roofline"] = mfma_roofline(wl.flops(), r["kernel_us_per_step"], traffic_for(wl.name), F32_PEAK_TFLOPS)
     elif wl.name.startswith("C5"):
         # Whole graph per call: the three quantized projections dominate; price all kernels of one
         # call against HBM.
@@ -237,7 +246,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--extra", default="C3,C4,C5,Q1,Q2,G1,G2,R1,D1", help="comma list of other configs to report under 'extra'")
+    ap.add_argument("--extra", default="C3,C4,C5,Q1,Q2,G1,G2,R1,R3,D1", help="comma list of other configs to report under 'extra'")
     ap.add_argument("--only", default="", help="run only this config (profiling passes); prints its entry")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-crossover", dest="crossover", action="store_false",

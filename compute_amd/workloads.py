@@ -374,6 +374,13 @@ def make(name: str, seed: int = 0) -> QDWorkload:
         x = bf16_from_f32(rx.standard_normal((M, K)).astype(np.float32))
         w = bf16_from_f32((rw.standard_normal((K, N)) * 0.02).astype(np.float32))
         return DotWorkload("D1_dotgeneral_bf16_prefill", M, K, N, x, w)
+    if name == "R3":  # the reference's own layout at prefill: f32 x [2048,4096], Int4, scale [K, N/128]
+        M, K, N, G = 2048, 4096, 11008, 128
+        x = rx.standard_normal((M, K)).astype(np.float32)
+        w = pack_int4(rw.integers(-8, 8, K * N))
+        s = rs.uniform(0.002, 0.02, (K, (N + G - 1) // G)).astype(np.float32)
+        return QDWorkload("R3_ref_layout_prefill_int4_f32", M, K, N, Float32, Int4, Float32, s.shape, 1, G, None, 0,
+                          x, w, s, None)
     if name in ("R1", "R2"):  # the reference's own layout at the C2 shape: f32 x, scale [K, N/128]
         M, K, N, G = 1, 4096, 11008, 128
         nf4 = name == "R2"

@@ -282,9 +282,10 @@ def _plan(backend, M, K, N, *, x_dtype, w_dtype, s_dtype, block_axis, block_size
 
 def test_qdense_plan_selection():
     """Which kernel each regime takes (host-only planning): the MFMA decode kernel for bf16 x with
-    K-blocked scales, the GEMV for the reference's own layout / f32 x / zero points / NF4 at
-    M <= 4, the MFMA GEMM at prefill, the reference-order kernel for small problems and for
-    everything with the "exact" option."""
+    K-blocked scales, the GEMV for the reference's own layout / f32 x / zero points / NF4 up to
+    64 rows, the MFMA GEMM at prefill, the f32 dequantise-and-contract path for the reference
+    layout past 64 rows, the reference-order kernel for small problems and for everything with
+    the "exact" option."""
     F32, BF16 = ca.Float32, ca.BFloat16
     for opts, exact in (("host_only", False), ("host_only,exact", True)):
         b = ca.New(opts)
@@ -322,16 +323,19 @@ def test_qdense_plan_selection():
                          block_size=4096) == want("qdense_gemm_mfma_u4")
             assert _plan(b, 2048, 4096, 14336, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=BF16, block_axis=0,
                          block_size=64) == want("qdense_gemm_mfma_i8_grouped")
-            # Groups that do not tile K in 64-row blocks stay on the reference-order kernel.
+            # Groups that do not tile K in 64-row blocks take the f32 dequantise-and-contract path.
             assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
-                         block_size=96) == "qdense_exact"
+                         block_size=96) == want("qdense_dequant_f32_mfma")
             # Small problems, M > 64 with the reference layout, unsupported block sizes: reference order.
             assert _plan(b, 1, 512, 1024, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=64) == "qdense_exact"
             assert _plan(b, 8, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=64) == want("qdense_gemv_i8")
+            # Past the GEMV's 64 rows, the reference layout dequantises into f32 for the matrix cores.
             assert _plan(b, 65, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
-                         block_size=64) == "qdense_exact"
+                         block_size=64) == want("qdense_dequant_f32_mfma")
+            assert _plan(b, 512, 4096, 4096, x_dtype=BF16, w_dtype=ca.Uint4, s_dtype=F32, block_axis=1,
+                         block_size=128, scheme=1) == want("qdense_dequant_f32_mfma")
             assert _plan(b, 1, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=16) == "qdense_exact"
         finally:
