@@ -159,7 +159,9 @@ __global__ __launch_bounds__(kExactThreads) void qdense_exact_kernel(QDenseDesc 
 // same x*(w*s + zp)); with the f32 sums in another order, the result stays within the f32
 // accumulation bound of the reference's.
 // =============================================================================================
-constexpr int64_t kDeqMinMKN = (int64_t)1 << 24;      // smaller problems keep the exact kernel
+// Problems of at most 2^24 multiply-adds keep the exact kernel (the reference's own
+// BenchmarkQuantizedDense shapes, up to 32 x 512 x 1024, stay bit-identical to it).
+constexpr int64_t kDeqMinMKN = (int64_t)1 << 24;
 constexpr int64_t kDeqMaxWeightBytes = (int64_t)8 << 30;  // f32 copy of the weights
 
 __global__ void qdense_dequant_f32_kernel(QDenseDesc d, float* __restrict__ wf) {
@@ -189,7 +191,7 @@ static bool qdense_dequant_fits(const QDenseDesc& d) {
   auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
   return (d.scheme == MX_QUANT_LINEAR || d.scheme == MX_QUANT_NF4) &&
          (d.x_dt == MX_DTYPE_FLOAT32 || d.x_dt == MX_DTYPE_BFLOAT16) && d.M > 4 && d.K % 4 == 0 &&
-         d.M * d.K * d.N >= kDeqMinMKN && d.K * d.N * 4 <= kDeqMaxWeightBytes && d.M < (1 << 24) &&
+         d.M * d.K * d.N > kDeqMinMKN && d.K * d.N * 4 <= kDeqMaxWeightBytes && d.M < (1 << 24) &&
          d.K < (1 << 24) && d.N < (1 << 24) && aligned(d.x, 16);
 }
 

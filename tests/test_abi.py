@@ -338,6 +338,13 @@ def test_qdense_plan_selection():
                          block_size=128, scheme=1) == want("qdense_dequant_f32_mfma")
             assert _plan(b, 1, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=16) == "qdense_exact"
+            # The reference's BenchmarkQuantizedDense shapes (at most 2^24 multiply-adds) keep the
+            # exact kernel; one row more takes the dequantise-and-contract path.
+            for scheme, w_dt in ((0, ca.Int8), (1, ca.Uint8)):
+                assert _plan(b, 32, 512, 1024, x_dtype=F32, w_dtype=w_dt, s_dtype=F32, block_axis=1,
+                             block_size=128, scheme=scheme) == "qdense_exact"
+                assert _plan(b, 33, 512, 1024, x_dtype=F32, w_dtype=w_dt, s_dtype=F32, block_axis=1,
+                             block_size=128, scheme=scheme) == want("qdense_dequant_f32_mfma")
         finally:
             b.Finalize()
     b = ca.New("host_only,gemv_over_gemm")
