@@ -20,6 +20,7 @@ MX_ERR_FINALIZED = -5
 MX_ERR_NO_DEVICE = -6
 
 MX_MAX_RANK = 8
+MX_QDENSE_NOALLOC_SCRATCH_BYTES = 16 << 20  # mxrt.h: the static per-GPU scratch of mx_qdense_noalloc
 
 
 class mx_shape(C.Structure):
@@ -144,6 +145,7 @@ SIGNATURES = {
     "mx_exec_describe": [_P, C.c_char_p, _SZ],
     "mx_qdense": [_P, C.POINTER(mx_qdense_args)],
     "mx_qdense_plan": [_P, C.POINTER(mx_qdense_args), C.c_char_p, _SZ],
+    "mx_qdense_noalloc": [_P, C.POINTER(mx_qdense_args)],
     "mx_quantized_embedding_lookup": [_P, C.POINTER(mx_qembed_args)],
 }
 

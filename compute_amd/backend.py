@@ -319,6 +319,10 @@ class Backend:
     def QDense(self, args: _lib.mx_qdense_args) -> None:
         _check(self._lib.mx_qdense(self._h, C.byref(args)))
 
+    def QDenseNoAlloc(self, args: _lib.mx_qdense_args) -> None:
+        """mx_qdense without device allocation (split-K scratch from a static per-GPU array)."""
+        _check(self._lib.mx_qdense_noalloc(self._h, C.byref(args)))
+
     def QDensePlan(self, args: _lib.mx_qdense_args) -> str:
         buf = C.create_string_buffer(128)
         _check(self._lib.mx_qdense_plan(self._h, C.byref(args), buf, len(buf)))

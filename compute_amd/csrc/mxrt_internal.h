@@ -129,6 +129,12 @@ struct mx_backend {
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
 
+  // The device's static scratch array for mx_qdense_noalloc (set up at backend creation), and
+  // whether such a call is in progress: then scratch comes from that array and nothing may
+  // allocate device memory.
+  void* noalloc_scratch = nullptr;
+  bool noalloc_active = false;
+
   // Profiling.
   bool profiling = false;
   std::vector<mx::PendingTiming> pending;
@@ -154,7 +160,11 @@ int check_device(mx_backend* b);
 int dev_alloc(mx_backend* b, size_t bytes, void** out);
 void dev_free(mx_backend* b, void* p);
 // Ensures scratch has at least `bytes` (zero-filled on growth). Returns the device pointer.
+// Inside mx_qdense_noalloc it returns the device's static array instead and never allocates.
 int ensure_scratch(mx_backend* b, size_t bytes, void** out);
+// Looks up this device's static scratch array for mx_qdense_noalloc (once per device) and keeps
+// its address in b->noalloc_scratch; b->device must be current.
+int noalloc_scratch_setup(mx_backend* b);
 
 // Launch wrapper: when profiling is on, the kernel launched inside `fn` (through dispatch())
 // carries a start/stop event pair that the runtime stamps with the kernel's own execution
@@ -175,14 +185,15 @@ int timing_end(mx_backend* b, const char* name, const LaunchEvents& ev);
 template <typename F>
 int launch(mx_backend* b, const char* name, F&& fn) {
   LaunchEvents ev;
-  if (b->profiling) MX_TRY(timing_begin(b, &ev));
+  const bool timed = b->profiling && !b->noalloc_active;
+  if (timed) MX_TRY(timing_begin(b, &ev));
   g_launch_events = ev;
   fn();
   g_launch_events = LaunchEvents{};
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(MX_ERR_HIP, "launch of %s failed: %s", name, hipGetErrorString(e));
-  if (b->profiling) MX_TRY(timing_end(b, name, ev));
+  if (timed) MX_TRY(timing_end(b, name, ev));
   return MX_OK;
 }
 

@@ -261,7 +261,9 @@ static QPath choose_path(const mx_backend* b, const QDenseDesc& d) {
   if (!b->gemv_over_gemm && qdense_gemm_fits(d)) return QPath::kGemm;
   if (qdense_gemv_fits(d)) return QPath::kGemv;
   if (qdense_gemm_fits(d)) return QPath::kGemm;
-  if (qdense_dequant_fits(d)) return QPath::kDequant;
+  // The dequantised f32 copy of the weights is a device allocation: without one the exact
+  // kernel runs (allocation-free, bit-identical to the reference).
+  if (!b->noalloc_active && qdense_dequant_fits(d)) return QPath::kDequant;
   return QPath::kExact;
 }
 

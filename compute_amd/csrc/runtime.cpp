@@ -202,6 +202,9 @@ int check_device(mx_backend* b) {
 
 int dev_alloc(mx_backend* b, size_t bytes, void** out) {
   MX_TRY(check_device(b));
+  if (b->noalloc_active)
+    return set_error(MX_ERR_INVALID, "mx_qdense_noalloc: this problem would allocate %zu bytes of device memory",
+                     bytes);
   return b->pool.alloc(bytes, out);
 }
 
@@ -210,6 +213,15 @@ void dev_free(mx_backend* b, void* p) {
 }
 
 int ensure_scratch(mx_backend* b, size_t bytes, void** out) {
+  if (b->noalloc_active) {
+    if (bytes > MX_QDENSE_NOALLOC_SCRATCH_BYTES)
+      return set_error(MX_ERR_INVALID,
+                       "mx_qdense_noalloc: the split-K scratch of this problem (%zu bytes) exceeds the "
+                       "static maximum of %u bytes; use mx_qdense",
+                       bytes, (unsigned)MX_QDENSE_NOALLOC_SCRATCH_BYTES);
+    *out = b->noalloc_scratch;
+    return MX_OK;
+  }
   if (b->scratch_bytes < bytes) {
     if (b->scratch) {
       MX_CHECK_HIP(hipStreamSynchronize(b->stream));
@@ -345,8 +357,14 @@ int mx_backend_new(const char* config, mx_backend** out) {
   hipDeviceProp_t prop;
   if (e == hipSuccess) e = hipGetDeviceProperties(&prop, device);
   if (e != hipSuccess) {
+    if (b->stream) (void)hipStreamDestroy(b->stream);
     delete b;
     return set_error(MX_ERR_HIP, "device init failed: %s", hipGetErrorString(e));
+  }
+  if (int rc = noalloc_scratch_setup(b); rc != MX_OK) {
+    (void)hipStreamDestroy(b->stream);
+    delete b;
+    return rc;
   }
   b->num_cus = prop.multiProcessorCount;
   char desc[512];

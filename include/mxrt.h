@@ -370,6 +370,19 @@ int mx_qdense(mx_backend* b, const mx_qdense_args* args);
 /* Name of the kernel family mx_qdense would pick for these arguments ("gemv_i4_dot2", ...). */
 int mx_qdense_plan(mx_backend* b, const mx_qdense_args* args, char* buf, size_t buflen);
 
+/* mx_qdense without any device allocation. No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). The split-K partial sums and arrival counters live in a static device array of
+ * MX_QDENSE_NOALLOC_SCRATCH_BYTES per GPU, set up by mx_backend_new and held until the process
+ * ends; a problem whose split-K needs more returns MX_ERR_INVALID before anything is launched.
+ * Results are bit-identical to mx_qdense's, except where mx_qdense would dequantise the weights
+ * into an f32 copy (reference layout at prefill size): that problem runs the exact kernel, whose
+ * result is bit-identical to the reference's. Every call on one GPU shares the array, from any
+ * backend: calls that overlap on one GPU (several streams or backends) race. Launches are not
+ * recorded in the backend's kernel profile. */
+#define MX_QDENSE_NOALLOC_SCRATCH_BYTES (16u << 20)
+int mx_qdense_noalloc(mx_backend* b, const mx_qdense_args* args);
+
 /* QuantizedEmbeddingLookup on device pointers (the Executable launches the same kernel);
  * replaces execQuantizedEmbeddingLookup (internal/gobackend/fusedops/quantizeddense.go:455-499).
  * Waits for the launch: an index outside [0, vocab) is reported as MX_ERR_INVALID. */

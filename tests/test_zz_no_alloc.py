@@ -1,0 +1,147 @@
+"""mx_qdense_noalloc (FusedQuantizedDense without device allocation) through the C ABI, against
+mx_qdense on the same device buffers.
+
+The allocation-free entry point runs mx_qdense's kernels with their split-K scratch taken from a
+static per-GPU array, so on the skinny, GEMV and GEMM paths its result must be bit-identical to
+mx_qdense's, and within the oracle bars of those paths (bf16 outputs rel 1e-2 / abs 1e-3 of the
+reference's f32 result).  Where mx_qdense dequantises the weights into an f32 copy, the
+allocation-free call runs the exact kernel: its result must equal the oracle's restatement of the
+reference loop bit for bit, and mx_qdense's within the f32 accumulation bound.  Each case makes two
+calls in a row, the second on a smaller problem, as a caller reusing the shared array would.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import compute_amd as ca
+from compute_amd import _lib
+from oracle import oracle as O
+from tests.qd_helpers import DT, assert_bf16_close, assert_f32_accumulation_close
+
+pytestmark = pytest.mark.gpu
+
+
+class Direct:
+    """A FusedQuantizedDense problem on device buffers, with one output buffer per entry point."""
+
+    def __init__(self, backend, p: O.QDenseProblem):
+        self.backend, self.p = backend, p
+        up = lambda a, sh: backend.BufferFromFlatData(0, np.ascontiguousarray(a).ravel(), sh)
+        self.x = up(p.x, ca.Shape(DT[p.x_dtype], p.M, p.K))
+        self.w = up(p.w, ca.Shape(DT[p.w_dtype], p.K, p.N))
+        self.s = up(p.scale, ca.Shape(DT[p.scale_dtype], *p.scale_shape))
+        self.zp = up(p.zp, ca.Shape(DT[p.zp_dtype], *p.scale_shape)) if p.zp is not None else None
+        self.bias = up(p.bias, ca.Shape(DT[p.bias_dtype], p.N)) if p.bias is not None else None
+        out_shape = ca.Shape(DT[p.x_dtype], p.M, p.N)
+        zeros = np.zeros(p.M * p.N, dtype=out_shape.dtype.numpy_storage())
+        self.outs = [up(zeros, out_shape) for _ in range(2)]
+
+    def args(self, out) -> _lib.mx_qdense_args:
+        p = self.p
+        a = _lib.mx_qdense_args()
+        a.x, a.w, a.scale = self.x.DevicePtr(), self.w.DevicePtr(), self.s.DevicePtr()
+        if self.zp is not None:
+            a.zero_point, a.zero_point_dtype = self.zp.DevicePtr(), p.zp_dtype
+        if self.bias is not None:
+            a.bias, a.bias_dtype = self.bias.DevicePtr(), p.bias_dtype
+        a.out = out.DevicePtr()
+        a.M, a.K, a.N = p.M, p.K, p.N
+        a.x_dtype, a.w_dtype, a.scale_dtype = p.x_dtype, p.w_dtype, p.scale_dtype
+        a.scheme, a.block_axis, a.block_size, a.activation = p.scheme, p.block_axis, p.block_size, p.act
+        return a
+
+    def call(self, entry: str, out) -> int:
+        lib = self.backend._lib
+        return getattr(lib, entry)(self.backend._h, C.byref(self.args(out)))
+
+    def run_both(self):
+        """(mx_qdense result, mx_qdense_noalloc result), each read back after the stream drains."""
+        for entry, out in zip(("mx_qdense", "mx_qdense_noalloc"), self.outs):
+            rc = self.call(entry, out)
+            assert rc == _lib.MX_OK, f"{entry}: {self.backend._lib.mx_last_error().decode()}"
+        shape = (self.p.M, self.p.N)
+        return tuple(o.ToFlatData().reshape(shape) for o in self.outs)
+
+
+def problem(M, K, N, seed, **kw):
+    kw.setdefault("bias", True)
+    kw.setdefault("scale_range", (0.002, 0.02))
+    return O.make_problem(M, K, N, seed=seed, **kw)
+
+
+# (first call, second smaller call) per kernel family; the plan of mx_qdense is asserted so each
+# pair exercises the path it names.
+SKINNY = [problem(4, 4096, 4096, 1, w_dtype=O.DT_INT4, block_axis=0, block_size=128),
+          problem(2, 2048, 1024, 2, w_dtype=O.DT_INT4, block_axis=0, block_size=128)]
+SKINNY_I8 = [problem(16, 4096, 14336, 3, w_dtype=O.DT_INT8, block_axis=0, block_size=64, act=O.ACT_SILU),
+             problem(1, 4096, 11008, 4, w_dtype=O.DT_INT8, block_axis=0, block_size=4096, per_channel_1d=True,
+                     scale_dtype=O.DT_FLOAT32)]
+GEMV = [problem(3, 4096, 2048, 5, w_dtype=O.DT_INT8, x_dtype=O.DT_FLOAT32, block_axis=0, block_size=64),
+        problem(2, 1024, 1024, 6, w_dtype=O.DT_INT8, x_dtype=O.DT_FLOAT32, block_axis=0, block_size=64)]
+GEMM = [problem(32, 1024, 2048, 7, w_dtype=O.DT_INT8, block_axis=0, block_size=1024, per_channel_1d=True,
+                scale_dtype=O.DT_FLOAT32),
+        problem(17, 512, 1024, 8, w_dtype=O.DT_INT8, block_axis=0, block_size=512, per_channel_1d=True,
+                scale_dtype=O.DT_FLOAT32)]
+
+
+@pytest.mark.parametrize("pair,plan", [(SKINNY, "qdense_skinny_mfma_i4"), (SKINNY_I8, "qdense_skinny_mfma_i8"),
+                                       (GEMV, "qdense_gemv_i8"), (GEMM, "qdense_gemm_mfma_i8")],
+                         ids=["skinny_i4", "skinny_i8", "gemv", "gemm"])
+def test_noalloc_matches_qdense(backend, pair, plan):
+    for p in pair:
+        d = Direct(backend, p)
+        assert backend.QDensePlan(d.args(d.outs[0])) == plan
+        ref, got = d.run_both()
+        assert np.array_equal(got, ref), f"{p.M}x{p.K}x{p.N}: mx_qdense_noalloc differs from mx_qdense"
+        want = O.qdense_f32(p, threads=8)
+        if p.x_dtype == O.DT_BFLOAT16:
+            assert_bf16_close(got, want, what=f"{p.M}x{p.K}x{p.N}")
+        else:
+            assert_f32_accumulation_close(got, p, what=f"{p.M}x{p.K}x{p.N}")
+
+
+def test_noalloc_reference_layout_runs_exact(backend):
+    """Reference layout at prefill size: mx_qdense dequantises into an f32 weight copy, the
+    allocation-free call runs the exact kernel (the reference's loop order)."""
+    pair = [problem(96, 512, 1024, 9, w_dtype=O.DT_INT4, x_dtype=O.DT_FLOAT32, block_axis=1, block_size=64),
+            problem(64, 512, 768, 10, w_dtype=O.DT_UINT8, x_dtype=O.DT_FLOAT32, block_axis=1, block_size=32,
+                    zp=True)]
+    for p in pair:
+        d = Direct(backend, p)
+        assert backend.QDensePlan(d.args(d.outs[0])) == "qdense_dequant_f32_mfma"
+        ref, got = d.run_both()
+        want = O.qdense_f32(p, threads=8)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "exact path differs from the reference loop"
+        assert_f32_accumulation_close(ref, p, what="mx_qdense (dequantised f32 weights)")
+
+
+def test_noalloc_rejects_oversized_scratch(backend):
+    """A skinny problem whose split-K tiles exceed the static array is refused before any
+    launch; the backend then keeps working on both entry points."""
+    M, K, N = 16, 32768, 8192  # 32 slices of [16, 8192] f32 partial tiles: 16 MiB + counters
+    p = O.QDenseProblem(M=M, K=K, N=N, x=np.zeros((M, K), np.uint16), w=np.zeros(K * N // 2, np.uint8),
+                        scale=np.zeros((K // 128, N), np.uint16), x_dtype=O.DT_BFLOAT16, w_dtype=O.DT_INT4,
+                        scale_dtype=O.DT_BFLOAT16, scale_shape=(K // 128, N), block_axis=0, block_size=128)
+    d = Direct(backend, p)
+    assert backend.QDensePlan(d.args(d.outs[0])).startswith("qdense_skinny_mfma")
+    rc = d.call("mx_qdense_noalloc", d.outs[1])
+    assert rc == _lib.MX_ERR_INVALID
+    msg = backend._lib.mx_last_error().decode()
+    assert "exceeds the static maximum" in msg and str(_lib.MX_QDENSE_NOALLOC_SCRATCH_BYTES) in msg
+    small = Direct(backend, SKINNY[1])
+    ref, got = small.run_both()
+    assert np.array_equal(got, ref)
+
+
+def test_noalloc_second_backend_shares_array():
+    """A second backend on the same GPU gets the same static array (set up once per device) and
+    computes the same result."""
+    b2 = ca.New("mi355x")
+    try:
+        d = Direct(b2, SKINNY[0])
+        ref, got = d.run_both()
+        assert np.array_equal(got, ref)
+        assert_bf16_close(got, O.qdense_f32(SKINNY[0], threads=8), what="second backend")
+    finally:
+        b2.Finalize()
