@@ -9,12 +9,16 @@
 // The products x*w are exact in f32 (bf16 x, |w| <= 255), so only the summation order differs
 // from the reference loop.
 //
-// The kernel is HBM-bound: every weight byte is read once.  It is "one-shot": every wave issues
-// all of its loads at entry (T steps of 32 K rows, T = 1, 2 or 4), straight into registers, so
-// the whole matrix is requested at once and each wave computes a step as soon as that step's
-// data has arrived.  A step is dequantised in registers into the B operand of
-// v_mfma_f32_16x16x32_bf16 (the matrix cores do the multiply-adds, the VALU only converts); the
-// 16 rows of the A operand are the rows of x (rows >= M repeat row M-1 and are never stored).
+// The kernel is HBM-bound: every weight byte is read once.  Each wave walks its T steps of 32 K
+// rows in a software pipeline with two steps in flight: as soon as a step has been computed, the
+// step two ahead is requested into the registers it used.  A step is dequantised in registers
+// into the B operand of v_mfma_f32_16x16x32_bf16 (the matrix cores do the multiply-adds, the VALU
+// only converts); the 16 rows of the A operand are the rows of x (rows >= M repeat row M-1 and
+// are never stored).  The code is kept short on purpose: a launch this brief runs its
+// instructions cold, so the main loop is a rolled loop (its body two steps, the last two steps
+// peeled so that every iteration issues the same loads and each wait is exact) and the output
+// code is one rolled loop with a short path for outputs without activation, pair or elementwise
+// operand.
 //
 // Lane layout (wave of 64 lanes, cg = lane % 16, kq = lane / 16).  A lane reads 8 bytes of each
 // of the rows k0 + 8*kq + e (e = 0..7) of a 32-row step: 16 int4 or 8 int8 columns (CPL), so a
@@ -27,18 +31,20 @@
 //   int8/uint8: exact conversion through f32 (a byte has at most 8 significant bits; the signed
 //               byte is selected and sign-extended by the conversion itself), the two high
 //               halves packed with one v_perm;
-//   int4/uint4: v_perm gathers the bytes of two rows, then and-or turns a nibble u into the
-//               bf16 bit pattern 0x4300|u = 128 + u (exact); Int4 first flips bit 3 of every
-//               nibble, giving 136 + w.  The offset is removed once per group with the group's
-//               row sums of x, which one extra MFMA against an all-ones B operand produces.
+//   int4/uint4: v_perm gathers the bytes of two rows, then one and-xor (v_bitop3) turns a
+//               nibble u into the bf16 bit pattern 0x4300|u = 128 + u (exact); for Int4 the same
+//               xor flips bit 3 of the nibble, giving 136 + w.  The offset is removed once per
+//               group with the group's row sums of x, which one extra MFMA against an all-ones B
+//               operand produces.
 //
 // Work decomposition.  The K steps of a column block are dealt out T at a time to waves, in
 // order; a workgroup of NW = 8 waves takes NW consecutive wave-chunks (one K slice), so a
-// column block has S = ceil(K/32 / (T*NW)) slices.  T divides the steps of a scale group, so a
-// wave stays inside one group and applies the group scale once, at its end.  The waves'
-// partial tiles are summed through LDS in wave order; with S > 1 every workgroup stores its
-// tile to scratch and the last one to arrive for the column block adds the S tiles in slice
-// order (deterministic), adds the bias, applies the activation and rounds to bf16.
+// column block has S = ceil(K/32 / (T*NW)) slices.  T is chosen per shape (the smallest even
+// divisor of K/32 that keeps the grid within one workgroup per CU).  A wave folds a group's
+// partial sums into its total with the group's scale when the group ends, or at its last step.
+// The waves' partial tiles are summed through LDS in wave order; with S > 1 every workgroup
+// stores its tile to scratch and the last one to arrive for the column block adds the S tiles in
+// slice order (deterministic), adds the bias, applies the activation and rounds to bf16.
 #include <algorithm>
 #include <cmath>
 
@@ -71,7 +77,10 @@ struct SkinnyArgs {
   const uint8_t* w2;
   const void* scale2;
   const void* bias2;
-  int M, K, N, G, S, act, s_dt, b_dt, res_dt, res_op;
+  int M, K, N;
+  int FS;  // K steps (32 rows) per scale group; K/32 for one scale per output column
+  int T;   // K steps per wave (the host makes K/32 a multiple of T)
+  int S, act, b_dt, res_dt, res_op;
   int pair, act2, b2_dt;
 };
 
@@ -115,20 +124,17 @@ __device__ __forceinline__ float sk_value(SkWord v, const void* p, int dt) {
   return dt == MX_DTYPE_BFLOAT16 ? __uint_as_float((v.w << v.shift) & 0xFFFF0000u) : __uint_as_float(v.w);
 }
 
-// WDT: weight dtype.  T: K steps per wave.  FL: steps per scale group seen by a wave (FL divides
-// T and the steps of a group, so a wave's groups are whole and aligned).  MR: rows of the MFMA
-// result kept per lane (1 when M == 1, else 4).
-// int8 grids have twice as many column blocks as int4 ones: their kernels are held to two
-// workgroups per CU (128 registers) so that a whole grid is resident at once.
-template <int WDT, int T, int FL, int MR>
-__global__ __launch_bounds__(kSkThreads)
-__attribute__((amdgpu_waves_per_eu((WDT == MX_DTYPE_INT8 || WDT == MX_DTYPE_UINT8) ? 4 : 1))) void
-qdense_skinny_kernel(SkinnyArgs a) {
-  static_assert(T % FL == 0, "whole scale groups per wave");
+// WDT: weight dtype.  MR: rows of the MFMA result kept per lane (1 when M == 1, else 4).
+// SF32: f32 scales (else bf16).  PIPE: T is even and two steps are in flight per wave (else
+// T == 1).  The main loop is a rolled loop whose body is two steps, so the code a CU fetches
+// stays small: a kernel this short-lived runs its instructions cold, and every instruction-cache
+// line it misses costs a trip to L2 or beyond.
+template <int WDT, int MR, bool SF32, bool PIPE>
+__global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a) {
   constexpr bool kI4 = WDT == MX_DTYPE_INT4 || WDT == MX_DTYPE_UINT4;
   constexpr int CPL = kI4 ? 2 * kSkLaneBytes : kSkLaneBytes;  // columns per lane
   constexpr int kCols = 16 * CPL;                              // columns per workgroup
-  constexpr int kSLoads = CPL * 4 / 16;  // 16-byte scale loads per lane (f32 size; bf16 repeats)
+  constexpr int kSLoads = CPL * (SF32 ? 4 : 2) / 16;           // 16-byte scale loads per step
   constexpr float kOff = WDT == MX_DTYPE_INT4 ? 136.0f : (WDT == MX_DTYPE_UINT4 ? 128.0f : 0.0f);
   extern __shared__ __attribute__((aligned(16))) float red[];
   __shared__ int s_last;
@@ -144,7 +150,7 @@ qdense_skinny_kernel(SkinnyArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int cg = lane & 15, kq = lane >> 4;
   const int KS = a.K >> 5;
-  const int wb = (slice * kSkWaves + wave) * T;  // first K step of this wave
+  const int k0 = (slice * kSkWaves + wave) * a.T;  // first K step of this wave
   const int cblk = cb * kCols;
   const int col0 = cblk + cg * CPL;
 
@@ -154,80 +160,73 @@ qdense_skinny_kernel(SkinnyArgs a) {
 #pragma unroll
     for (int r = 0; r < MR; ++r) tot[c][r] = 0.0f;
 
-  // The host makes K/32 a multiple of T, so a wave has T steps or none; with a fixed count the
-  // loads are one straight-line sequence and every step waits only for its own data.
-  if (wb < KS) {
+  if (k0 < KS) {
     // Lanes whose columns lie past N read column 0 instead (their results are never stored).
     const size_t row_bytes = kI4 ? (size_t)(a.N >> 1) : (size_t)a.N;
-    const size_t lbyte = (kI4 ? (size_t)(col0 >> 1) : (size_t)col0);
-    const uint8_t* wp = wmat + (size_t)(32 * wb + 8 * kq) * row_bytes + (lbyte + kSkLaneBytes <= row_bytes ? lbyte : 0);
-    const uint16_t* xp = a.x + (size_t)min(cg, a.M - 1) * a.K + 32 * wb + 8 * kq;
-    const int sb = a.s_dt == MX_DTYPE_BFLOAT16 ? 2 : 4;
-    const int scol = col0 < a.N ? col0 : 0;
-    const char* sp = (const char*)smat + (size_t)scol * sb;
-    const int s_last_load = CPL * sb / 16 - 1;
+    const size_t lbyte = kI4 ? (size_t)(col0 >> 1) : (size_t)col0;
+    const uint8_t* wp = wmat + (size_t)(8 * kq) * row_bytes + (lbyte + kSkLaneBytes <= row_bytes ? lbyte : 0);
+    const uint16_t* xp = a.x + (size_t)min(cg, a.M - 1) * a.K + 8 * kq;
+    const char* sp = (const char*)smat + (size_t)(col0 < a.N ? col0 : 0) * (SF32 ? 4 : 2);
+    const size_t srow = (size_t)a.N * (SF32 ? 4 : 2);
 
-    // Per scale group: its steps' x and weights, then its scales (needed only after its last
-    // step), so that a group's flush waits for nothing of the later groups.  Always kSLoads
-    // scale loads (bf16 scales repeat their last one): the number of loads in flight is fixed.
-    u32x4_v xv[T];
-    u32x2_v wv[T][8];
-    u32x4_v sv[T / FL][kSLoads];
+    // One step's operands: x (16 bytes), eight 8-byte weight row segments, and the scales of the
+    // step's group (loaded with every step, so that every step issues the same loads and each
+    // wait is exact; the repeats within a group hit the cache).
+    struct Slot {
+      u32x4_v x;
+      u32x2_v w[8];
+      u32x4_v s[kSLoads];
+    };
+    int ig = k0 / a.FS, irem = a.FS - k0 % a.FS;  // group and steps left in it, issue order
+    auto issue = [&](Slot& sl, int k) __attribute__((always_inline)) {
+      sl.x = *(const u32x4_v*)(xp + 32 * k);
+      const uint8_t* wk = wp + (size_t)(32 * k) * row_bytes;
 #pragma unroll
-    for (int f = 0; f < T / FL; ++f) {
+      for (int e = 0; e < 8; ++e) sl.w[e] = __builtin_nontemporal_load((const u32x2_v*)(wk + (size_t)e * row_bytes));
+      const char* sg = sp + (size_t)ig * srow;
 #pragma unroll
-      for (int tt = 0; tt < FL; ++tt) {
-        const int t = f * FL + tt;
-        xv[t] = *(const u32x4_v*)(xp + 32 * t);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          wv[t][e] = __builtin_nontemporal_load((const u32x2_v*)(wp + (size_t)(32 * t + e) * row_bytes));
+      for (int q = 0; q < kSLoads; ++q) sl.s[q] = *(const u32x4_v*)(sg + 16 * q);
+      if (--irem == 0) {
+        ++ig;
+        irem = a.FS;
       }
-      const char* sg = sp + (size_t)((32 * (wb + f * FL)) / a.G) * a.N * sb;
-#pragma unroll
-      for (int q = 0; q < kSLoads; ++q) sv[f][q] = *(const u32x4_v*)(sg + 16 * min(q, s_last_load));
-    }
-    // Keep every load above this point: the scheduler would otherwise interleave later steps'
-    // loads with earlier steps' arithmetic to save registers, and serialise their latencies.
-    __builtin_amdgcn_sched_barrier(0);
+    };
 
+    // A nibble u (bits 0-3 and 16-19 after the mask) becomes the bf16 pattern 0x4300 | u =
+    // 128 + u with one xor (the mask leaves no other bits); for Int4 the same xor also flips bit 3
+    // of the nibble, giving 136 + w.  (x & m) ^ c is one v_bitop3_b32.
     const uint32_t kMask = 0x000F000Fu;
-    const uint32_t kOr = vgpr_const(0x43004300u);
+    const uint32_t kOr = vgpr_const(WDT == MX_DTYPE_INT4 ? 0x43084308u : 0x43004300u);
     const u32x4_v ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
     const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4_t grp[CPL], sx = zero;
 #pragma unroll
-    for (int f = 0; f < T / FL; ++f) {
-#pragma unroll
-    for (int tt = 0; tt < FL; ++tt) {
-      const int t = f * FL + tt;
+    for (int c = 0; c < CPL; ++c) grp[c] = zero;
+    // A step: dequantise into MFMA B operands and accumulate the group's partial sums.
+    auto compute = [&](const Slot& sl) __attribute__((always_inline)) {
       if constexpr (kI4) {
 #pragma unroll
         for (int d = 0; d < CPL / 8; ++d) {
           uint32_t bq[8][4];  // columns 8d + 0..7, four pair-dwords each
 #pragma unroll
           for (int pp = 0; pp < 4; ++pp) {
-            uint32_t A = wv[t][2 * pp][d], B = wv[t][2 * pp + 1][d];
-            if constexpr (WDT == MX_DTYPE_INT4) {
-              A ^= 0x88888888u;
-              B ^= 0x88888888u;
-            }
+            const uint32_t A = sl.w[2 * pp][d], B = sl.w[2 * pp + 1][d];
             const uint32_t t0 = __builtin_amdgcn_perm(B, A, 0x06040200u);  // [A.b0, A.b2, B.b0, B.b2]
             const uint32_t t1 = __builtin_amdgcn_perm(B, A, 0x07050301u);  // [A.b1, A.b3, B.b1, B.b3]
-            bq[0][pp] = (t0 & kMask) | kOr;
-            bq[1][pp] = ((t0 >> 4) & kMask) | kOr;
-            bq[4][pp] = ((t0 >> 8) & kMask) | kOr;
-            bq[5][pp] = ((t0 >> 12) & kMask) | kOr;
-            bq[2][pp] = (t1 & kMask) | kOr;
-            bq[3][pp] = ((t1 >> 4) & kMask) | kOr;
-            bq[6][pp] = ((t1 >> 8) & kMask) | kOr;
-            bq[7][pp] = ((t1 >> 12) & kMask) | kOr;
+            bq[0][pp] = (t0 & kMask) ^ kOr;
+            bq[1][pp] = ((t0 >> 4) & kMask) ^ kOr;
+            bq[4][pp] = ((t0 >> 8) & kMask) ^ kOr;
+            bq[5][pp] = ((t0 >> 12) & kMask) ^ kOr;
+            bq[2][pp] = (t1 & kMask) ^ kOr;
+            bq[3][pp] = ((t1 >> 4) & kMask) ^ kOr;
+            bq[6][pp] = ((t1 >> 8) & kMask) ^ kOr;
+            bq[7][pp] = ((t1 >> 12) & kMask) ^ kOr;
           }
 #pragma unroll
           for (int c = 0; c < 8; ++c)
-            grp[8 * d + c] = sk_mfma(xv[t], u32x4_v{bq[c][0], bq[c][1], bq[c][2], bq[c][3]}, tt == 0 ? zero : grp[8 * d + c]);
+            grp[8 * d + c] = sk_mfma(sl.x, u32x4_v{bq[c][0], bq[c][1], bq[c][2], bq[c][3]}, grp[8 * d + c]);
         }
-        sx = sk_mfma(xv[t], ones, tt == 0 ? zero : sx);
+        sx = sk_mfma(sl.x, ones, sx);
       } else {
 #pragma unroll
         for (int d = 0; d < CPL / 4; ++d) {
@@ -236,7 +235,7 @@ qdense_skinny_kernel(SkinnyArgs a) {
             uint32_t bq[4];
 #pragma unroll
             for (int pp = 0; pp < 4; ++pp) {
-              const uint32_t r0 = wv[t][2 * pp][d], r1 = wv[t][2 * pp + 1][d];
+              const uint32_t r0 = sl.w[2 * pp][d], r1 = sl.w[2 * pp + 1][d];
               float f0, f1;
               if constexpr (WDT == MX_DTYPE_INT8) {
                 f0 = (float)(int8_t)(r0 >> (8 * c));
@@ -247,35 +246,75 @@ qdense_skinny_kernel(SkinnyArgs a) {
               }
               bq[pp] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
             }
-            grp[4 * d + c] = sk_mfma(xv[t], u32x4_v{bq[0], bq[1], bq[2], bq[3]}, tt == 0 ? zero : grp[4 * d + c]);
+            grp[4 * d + c] = sk_mfma(sl.x, u32x4_v{bq[0], bq[1], bq[2], bq[3]}, grp[4 * d + c]);
           }
         }
       }
-      }
-    // The group's scale, once per group: tot += (grp - offset * rowsum(x)) * s.
-    float sc[CPL];
-    if (a.s_dt == MX_DTYPE_BFLOAT16) {
+    };
+    // The group's scale, once per group (or at the end of the wave's steps):
+    // tot += (grp - offset * rowsum(x)) * s, then the group sums start again from zero.
+    auto fold = [&](const Slot& sl) __attribute__((always_inline)) {
+      float sc[CPL];
+      if constexpr (SF32) {
 #pragma unroll
-      for (int c = 0; c < CPL; c += 2) {
-        const uint32_t v = sv[f][c / 8][(c / 2) % 4];
-        sc[c] = __uint_as_float(v << 16);
-        sc[c + 1] = __uint_as_float(v & 0xFFFF0000u);
+        for (int c = 0; c < CPL; ++c) sc[c] = __uint_as_float(sl.s[c / 4][c % 4]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; c += 2) {
+          const uint32_t v = sl.s[c / 8][(c / 2) % 4];
+          sc[c] = __uint_as_float(v << 16);
+          sc[c + 1] = __uint_as_float(v & 0xFFFF0000u);
+        }
       }
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+          tot[c][r] = __builtin_fmaf(kOff != 0.0f ? grp[c][r] - kOff * sx[r] : grp[c][r], sc[c], tot[c][r]);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) grp[c] = zero;
+      sx = zero;
+    };
+    int crem = a.FS - k0 % a.FS;  // steps left in the current group, compute order
+    auto step = [&](const Slot& sl, int t) __attribute__((always_inline)) {
+      compute(sl);
+      if (--crem == 0 || t == a.T - 1) {
+        fold(sl);
+        if (crem == 0) crem = a.FS;
+      }
+    };
+
+    if constexpr (PIPE) {
+      // Two slots: step t + 2 is issued into a slot as soon as step t has used it, so each
+      // wave keeps two steps of loads in flight while it computes.  The last two steps are
+      // peeled off the loop so that every loop iteration issues the same loads.
+      Slot A, B;
+      issue(A, k0);
+      issue(B, k0 + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      int t = 0;
+#pragma unroll 1
+      for (; t < a.T - 2; t += 2) {
+        step(A, t);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(A, k0 + t + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        step(B, t + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(B, k0 + t + 3);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      step(A, t);
+      step(B, t + 1);
     } else {
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) sc[c] = __uint_as_float(sv[f][c / 4][c % 4]);
-    }
-#pragma unroll
-    for (int c = 0; c < CPL; ++c)
-#pragma unroll
-      for (int r = 0; r < MR; ++r)
-        tot[c][r] = __builtin_fmaf(kOff != 0.0f ? grp[c][r] - kOff * sx[r] : grp[c][r], sc[c], tot[c][r]);
+      Slot A;
+      issue(A, k0);
+      step(A, 0);
     }
   }
 
   // Every wave's tile (rows < M) into LDS as [waves][M][kCols]; each output then adds the waves
-  // in a fixed order.  Outputs are handled in quads (4 consecutive columns of one row): thread t
-  // owns quads g = t + i * kSkThreads of the block's M x kCols tile.
+  // in a fixed order.  Outputs are handled in quads (4 consecutive columns of one row).
   const int M = a.M;
   {
     float* rw = red + (size_t)wave * M * kCols;
@@ -289,125 +328,125 @@ qdense_skinny_kernel(SkinnyArgs a) {
       }
     }
   }
-  constexpr int kQPR = kCols / 4;                                    // quads per tile row
-  constexpr int kMaxQuads = kSkMaxRows * kQPR / kSkThreads;           // quads per thread (M = 16)
+  __syncthreads();
+  constexpr int kQPR = kCols / 4;  // quads per tile row
   const int t = threadIdx.x;
   const int MC = M * kCols, NQ = M * kQPR;
-  // Epilogue operands of a quad (bias, and the folded elementwise operand or the pair's second
-  // bias), loaded unconditionally (clamped into range) so that they travel with the loads they
-  // are issued beside.
-  struct QuadOps {
-    SkWord b[4], r[4];
-  };
-  auto quad_ops = [&](int m, int col) {
-    QuadOps q;
-    const int c = min(col, a.N - 4);
+  auto wave_sum = [&](int g) __attribute__((always_inline)) {
+    f32x4_t y = *(const f32x4_t*)(red + 4 * g);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      q.b[e] = sk_word(a.bias, c + e, a.b_dt, a.x);
-      q.r[e] = a.pair ? sk_word(a.bias2, c + e, a.b2_dt, a.x)
-                      : sk_word(a.res_op ? a.res : nullptr, (size_t)m * a.N + c + e, a.res_dt, a.x);
-    }
-    return q;
-  };
-  // bias, activation, bf16, the folded elementwise op or the pair product (each rounded as the
-  // separate ops round it), and one 8-byte store of the quad.
-  auto finish_quad = [&](int m, int col, f32x4_t y, f32x4_t y2, const QuadOps& q) {
-    if (col >= a.N) return;
-    uint16_t o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      o[e] = f32_to_bf16(act_fast(y[e] + sk_value(q.b[e], a.bias, a.b_dt), a.act));
-      if (a.pair) {
-        const uint16_t g = f32_to_bf16(act_fast(y2[e] + sk_value(q.r[e], a.bias2, a.b2_dt), a.act2));
-        o[e] = f32_to_bf16(mul_rn(bf16_to_f32(o[e]), bf16_to_f32(g)));
-      } else if (a.res_op) {
-        const float v = bf16_to_f32(o[e]), r = sk_value(q.r[e], a.res, a.res_dt);
-        o[e] = f32_to_bf16(a.res_op == MX_OP_MUL ? mul_rn(v, r) : add_rn(v, r));
-      }
-    }
-    *(u32x2_v*)(a.out + (size_t)m * a.N + col) = u32x2_v{o[0] | (uint32_t)o[1] << 16, o[2] | (uint32_t)o[3] << 16};
+    for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
+    return y;
   };
 
-  if (SP == 1) {
-    QuadOps ops[kMaxQuads];
-#pragma unroll
-    for (int i = 0; i < kMaxQuads; ++i) {
-      const int g = min(t + i * kSkThreads, NQ - 1);
-      ops[i] = quad_ops(g / kQPR, cblk + 4 * (g % kQPR));
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kMaxQuads; ++i) {
-      const int g = t + i * kSkThreads;
-      if (g < NQ) {
-        f32x4_t y = *(const f32x4_t*)(red + 4 * g);
-#pragma unroll
-        for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
-        finish_quad(g / kQPR, cblk + 4 * (g % kQPR), y, y, ops[i]);
-      }
-    }
-    return;
-  }
-  __syncthreads();
-
-  // Split K (or pair mode): store this work item's tile as [matrix][slice][M][N] (16-byte stores
-  // with the agent-scope coherence bit sc1: visible across the XCDs' L2s without whole-cache
-  // maintenance), wait until the stores have completed, then count the arrival.  Only the last
-  // arriver reads the tiles back, with loads that carry the same bit.
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
       a.partial, (short)0, (int)((size_t)SP * M * a.N * sizeof(float)), 0x00020000);
   constexpr int kSc1 = 16;  // cache-policy operand of the buffer intrinsics: sc1
-#pragma unroll
-  for (int i = 0; i < kMaxQuads; ++i) {
-    const int g = t + i * kSkThreads;
-    const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
-    if (g < NQ && col < a.N) {
-      f32x4_t y = *(const f32x4_t*)(red + 4 * g);
-#pragma unroll
-      for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, y), prs,
-                                            (unsigned)(((part * M + m) * a.N + col) * 4), 0, kSc1);
+  if (SP > 1) {
+    // Split K (or pair mode): store this work item's tile as [matrix][slice][M][N] (16-byte
+    // stores with the agent-scope coherence bit sc1: visible across the XCDs' L2s without
+    // whole-cache maintenance), wait until the stores have completed, then count the arrival.
+    // Only the last arriver reads the tiles back, with loads that carry the same bit.
+#pragma unroll 1
+    for (int g = t; g < NQ; g += kSkThreads) {
+      const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
+      if (col < a.N)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, wave_sum(g)), prs,
+                                              (unsigned)(((part * M + m) * a.N + col) * 4), 0, kSc1);
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev == (uint32_t)SP - 1u;
+      if (last) __hip_atomic_store(&a.counters[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&a.counters[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == (uint32_t)SP - 1u;
-    if (last) __hip_atomic_store(&a.counters[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  // Last arriver: each quad's SP partial tiles, kSl per batch of loads (all in flight together),
-  // added in slice order per matrix (from 0 when S > 1, as the split single product adds them;
-  // a pair with S = 1 takes each matrix's one tile as it is, as the unsplit kernel does).
-  constexpr int kSl = 16;
+
+  // The outputs of the column block: the sum of the waves' tiles (one work item) or of the
+  // partial tiles in slice order per matrix (each matrix's first tile taken as it is), then bias,
+  // activation, bf16, and the folded elementwise op or the pair product, each rounded as the
+  // separate ops round it, and one 8-byte store per quad.  The partial tiles are requested first
+  // and the epilogue operands only when they exist, so that their latencies overlap; the plain
+  // case (bias at most) takes a short path of its own, so that the activation code is not fetched.
+  constexpr int kSl = 8;  // partial tiles per batch of loads (all in flight together)
+  const bool plain = a.act == MX_ACT_NONE && !a.pair && !a.res_op;
+#pragma unroll 1
   for (int g = t; g < NQ; g += kSkThreads) {
     const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
-    const int c = min(col, a.N - 4);
-    f32x4_t y = {0.0f, 0.0f, 0.0f, 0.0f}, y2 = y;
-    QuadOps ops;
-    for (int s0 = 0; s0 < SP; s0 += kSl) {
-      f32x4_t v[kSl];
+    if (col >= a.N) continue;
+    f32x4_t y, y2;
+    if (SP == 1) {
+      y = wave_sum(g);
+      y2 = y;
+    } else {
+      y = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      y2 = y;
+#pragma unroll 1
+      for (int s0 = 0; s0 < SP; s0 += kSl) {
+        f32x4_t v[kSl];
 #pragma unroll
-      for (int u = 0; u < kSl; ++u) {
-        const int s = min(s0 + u, SP - 1);
-        v[u] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                               prs, (unsigned)(((s * M + m) * a.N + c) * 4), 0, kSc1));
-      }
-      if (s0 == 0) ops = quad_ops(m, col);
+        for (int u = 0; u < kSl; ++u)
+          v[u] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 prs, (unsigned)(((min(s0 + u, SP - 1) * M + m) * a.N + col) * 4), 0, kSc1));
 #pragma unroll
-      for (int u = 0; u < kSl; ++u) {
-        const int s = s0 + u;
-        if (s < a.S)
-          y = a.S == 1 ? v[u] : y + v[u];
-        else if (s < SP)
-          y2 = a.S == 1 ? v[u] : y2 + v[u];
+        for (int u = 0; u < kSl; ++u) {
+          const int s = s0 + u;
+          if (s < a.S)
+            y = s == 0 ? v[u] : y + v[u];
+          else if (s < SP)
+            y2 = s == a.S ? v[u] : y2 + v[u];
+        }
       }
     }
-    finish_quad(m, col, y, y2, ops);
+    f32x4_t pre = y;
+    if (a.bias) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pre[e] = y[e] + sk_value(sk_word(a.bias, col + e, a.b_dt, a.bias), a.bias, a.b_dt);
+    }
+    uint32_t o0, o1;
+    if (plain) {
+      o0 = (uint32_t)f32_to_bf16(pre[0]) | (uint32_t)f32_to_bf16(pre[1]) << 16;
+      o1 = (uint32_t)f32_to_bf16(pre[2]) | (uint32_t)f32_to_bf16(pre[3]) << 16;
+    } else {
+      // The pair's second pre-activation value, or the elementwise operand.
+      f32x4_t sec = y2;
+      if (a.pair) {
+        if (a.bias2) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            sec[e] = y2[e] + sk_value(sk_word(a.bias2, col + e, a.b2_dt, a.bias2), a.bias2, a.b2_dt);
+        }
+      } else if (a.res_op) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          sec[e] = sk_value(sk_word(a.res, (size_t)m * a.N + col + e, a.res_dt, a.res), a.res, a.res_dt);
+      }
+      o0 = 0u;
+      o1 = 0u;
+#pragma unroll 1
+      for (int e = 0; e < 4; ++e) {
+        const float pe = e == 0 ? pre[0] : e == 1 ? pre[1] : e == 2 ? pre[2] : pre[3];
+        const float se = e == 0 ? sec[0] : e == 1 ? sec[1] : e == 2 ? sec[2] : sec[3];
+        uint16_t v = f32_to_bf16(act_fast(pe, a.act));
+        if (a.pair) {
+          const uint16_t gv = f32_to_bf16(act_fast(se, a.act2));
+          v = f32_to_bf16(mul_rn(bf16_to_f32(v), bf16_to_f32(gv)));
+        } else if (a.res_op) {
+          const float vf = bf16_to_f32(v);
+          v = f32_to_bf16(a.res_op == MX_OP_MUL ? mul_rn(vf, se) : add_rn(vf, se));
+        }
+        const uint32_t sh = 16u * (uint32_t)(e & 1);
+        if (e < 2)
+          o0 |= (uint32_t)v << sh;
+        else
+          o1 |= (uint32_t)v << sh;
+      }
+    }
+    *(u32x2_v*)(a.out + (size_t)m * a.N + col) = u32x2_v{o0, o1};
   }
 }
 
@@ -420,47 +459,48 @@ bool qdense_skinny_fits(const QDenseDesc& d) {
   return d.M >= 1 && d.M <= kSkMaxRows && d.x_dt == MX_DTYPE_BFLOAT16 && d.scheme == MX_QUANT_LINEAR && !d.zp &&
          d.block_axis == 0 && d.K >= 32 && d.K % 32 == 0 && G % 32 == 0 && d.N >= 16 &&
          d.N % (dtype_is_packed(d.w_dt) ? 32 : 16) == 0 && d.K < (int64_t)1 << 30 && d.N < (int64_t)1 << 30 &&
-         aligned(d.w, 16) && aligned(d.x, 16) && aligned(d.scale, 16) && aligned(d.out, 8) &&
+         (d.s_dt == MX_DTYPE_BFLOAT16 || d.s_dt == MX_DTYPE_FLOAT32) && aligned(d.w, 16) && aligned(d.x, 16) &&
+         aligned(d.scale, 16) && aligned(d.out, 8) &&
          (!d.pair || (aligned(d.w2, 16) && aligned(d.scale2, 16) && d.res_op == 0));
 }
 
-// Steps per wave T and steps per scale group seen by a wave FL (FL divides T and the steps of a
-// group; a per-output-channel scale is one group spanning K): T = 4 when K/32 allows it and a
-// group holds an even number of steps, else T = FL = 1.  (T = 4 over four 32-row groups would hold
-// four groups' scales in registers.)
-struct SkSteps {
-  int T = 1, FL = 1;
-};
-
-static SkSteps skinny_steps(const QDenseDesc& d) {
+// Steps per wave T: 1 when K/32 is odd; else the smallest even divisor of K/32 whose grid (column
+// blocks x slices) is at most one workgroup per CU, so that the whole grid is resident at once
+// (the largest even divisor when none is).  T fixes the summation order, so it depends on the
+// shape of one product only: a pair launch sums each product exactly as its own launch would.
+static int skinny_steps(const QDenseDesc& d, int64_t nb, int num_cus) {
   const int64_t ks = d.K / 32;
-  const int64_t G = std::min<int64_t>(d.block_size, d.K);
-  const int64_t spg = G >= d.K ? ks : G / 32;
-  SkSteps r;
-  if (ks % 4 == 0 && spg % 2 == 0) {
-    r.T = 4;
-    r.FL = spg % 4 == 0 ? 4 : 2;
+  if (ks % 2 != 0) return 1;
+  int64_t best = 0;
+  for (int64_t T = 2; T <= ks; T += 2) {
+    if (ks % T != 0) continue;
+    best = T;
+    const int64_t S = (ks / T + kSkWaves - 1) / kSkWaves;
+    if (nb * S <= num_cus) break;
   }
-  return r;
+  return (int)best;
 }
 
-template <int WDT, int T, int FL>
-static void launch_fl(const SkinnyArgs& ga, int grid, size_t lds, hipStream_t st) {
-  if (ga.M == 1)
-    dispatch(qdense_skinny_kernel<WDT, T, FL, 1>, grid, kSkThreads, lds, st, ga);
+template <int WDT, int MR, bool SF32>
+static void launch_pipe(const SkinnyArgs& ga, int grid, size_t lds, hipStream_t st) {
+  if (ga.T >= 2)
+    dispatch(qdense_skinny_kernel<WDT, MR, SF32, true>, grid, kSkThreads, lds, st, ga);
   else
-    dispatch(qdense_skinny_kernel<WDT, T, FL, 4>, grid, kSkThreads, lds, st, ga);
+    dispatch(qdense_skinny_kernel<WDT, MR, SF32, false>, grid, kSkThreads, lds, st, ga);
 }
 
 template <int WDT>
-static void launch_skinny(const SkinnyArgs& ga, SkSteps sp, int grid, size_t lds, hipStream_t st) {
-  if (sp.T == 4) {
-    if (sp.FL == 4)
-      launch_fl<WDT, 4, 4>(ga, grid, lds, st);
+static void launch_skinny(const SkinnyArgs& ga, bool sf32, int grid, size_t lds, hipStream_t st) {
+  if (ga.M == 1) {
+    if (sf32)
+      launch_pipe<WDT, 1, true>(ga, grid, lds, st);
     else
-      launch_fl<WDT, 4, 2>(ga, grid, lds, st);
+      launch_pipe<WDT, 1, false>(ga, grid, lds, st);
   } else {
-    launch_fl<WDT, 1, 1>(ga, grid, lds, st);
+    if (sf32)
+      launch_pipe<WDT, 4, true>(ga, grid, lds, st);
+    else
+      launch_pipe<WDT, 4, false>(ga, grid, lds, st);
   }
 }
 
@@ -468,8 +508,8 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   const bool i4 = dtype_is_packed(d.w_dt);
   const int64_t cols = i4 ? 256 : 128;
   const int64_t nb = (d.N + cols - 1) / cols;
-  const SkSteps sp = skinny_steps(d);
-  const int64_t chunks = d.K / 32 / sp.T;  // wave-sized pieces of one column block
+  const int T = skinny_steps(d, nb, b->num_cus > 0 ? b->num_cus : 256);
+  const int64_t chunks = d.K / 32 / T;  // wave-sized pieces of one column block
   const int64_t S = (chunks + kSkWaves - 1) / kSkWaves;
   const int64_t SP = d.pair ? 2 * S : S;  // partial tiles per column block
   const size_t counter_bytes = 64 * 1024;
@@ -492,10 +532,10 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.M = (int)d.M;
   ga.K = (int)d.K;
   ga.N = (int)d.N;
-  ga.G = (int)std::min<int64_t>(d.block_size, d.K);
+  ga.FS = (int)(std::min<int64_t>(d.block_size, d.K) / 32);
+  ga.T = T;
   ga.S = (int)S;
   ga.act = d.act;
-  ga.s_dt = d.s_dt;
   ga.b_dt = d.b_dt;
   ga.res = d.res;
   ga.res_dt = d.res_dt;
@@ -509,13 +549,14 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   const int grid = (int)(nb * SP);
   // LDS: the waves' tiles [waves][M][cols].
   const size_t lds = (size_t)kSkWaves * d.M * cols * sizeof(float);
+  const bool sf32 = d.s_dt == MX_DTYPE_FLOAT32;
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     switch (d.w_dt) {
-      case MX_DTYPE_INT4: launch_skinny<MX_DTYPE_INT4>(ga, sp, grid, lds, st); break;
-      case MX_DTYPE_UINT4: launch_skinny<MX_DTYPE_UINT4>(ga, sp, grid, lds, st); break;
-      case MX_DTYPE_INT8: launch_skinny<MX_DTYPE_INT8>(ga, sp, grid, lds, st); break;
-      default: launch_skinny<MX_DTYPE_UINT8>(ga, sp, grid, lds, st); break;
+      case MX_DTYPE_INT4: launch_skinny<MX_DTYPE_INT4>(ga, sf32, grid, lds, st); break;
+      case MX_DTYPE_UINT4: launch_skinny<MX_DTYPE_UINT4>(ga, sf32, grid, lds, st); break;
+      case MX_DTYPE_INT8: launch_skinny<MX_DTYPE_INT8>(ga, sf32, grid, lds, st); break;
+      default: launch_skinny<MX_DTYPE_UINT8>(ga, sf32, grid, lds, st); break;
     }
   });
 }

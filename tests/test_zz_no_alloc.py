@@ -117,14 +117,14 @@ def test_noalloc_reference_layout_runs_exact(backend):
 
 
 def test_noalloc_rejects_oversized_scratch(backend):
-    """A skinny problem whose split-K tiles exceed the static array is refused before any
-    launch; the backend then keeps working on both entry points."""
-    M, K, N = 16, 32768, 8192  # 32 slices of [16, 8192] f32 partial tiles: 16 MiB + counters
-    p = O.QDenseProblem(M=M, K=K, N=N, x=np.zeros((M, K), np.uint16), w=np.zeros(K * N // 2, np.uint8),
-                        scale=np.zeros((K // 128, N), np.uint16), x_dtype=O.DT_BFLOAT16, w_dtype=O.DT_INT4,
-                        scale_dtype=O.DT_BFLOAT16, scale_shape=(K // 128, N), block_axis=0, block_size=128)
+    """A GEMV problem whose split-K tiles exceed the static array is refused before any launch;
+    the backend then keeps working on both entry points."""
+    M, K, N = 4, 32768, 8192  # 128 slices of [4, 8192] f32 partial tiles: 16 MiB + counters
+    p = O.QDenseProblem(M=M, K=K, N=N, x=np.zeros((M, K), np.float32), w=np.zeros(K * N // 2, np.uint8),
+                        scale=np.zeros((K // 128, N), np.float32), x_dtype=O.DT_FLOAT32, w_dtype=O.DT_INT4,
+                        scale_dtype=O.DT_FLOAT32, scale_shape=(K // 128, N), block_axis=0, block_size=128)
     d = Direct(backend, p)
-    assert backend.QDensePlan(d.args(d.outs[0])).startswith("qdense_skinny_mfma")
+    assert backend.QDensePlan(d.args(d.outs[0])).startswith("qdense_gemv")
     rc = d.call("mx_qdense_noalloc", d.outs[1])
     assert rc == _lib.MX_ERR_INVALID
     msg = backend._lib.mx_last_error().decode()
