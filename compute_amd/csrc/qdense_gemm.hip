@@ -9,7 +9,9 @@
 // with one group for per-channel scales; every product x*w is exact in f32 (bf16 x, |w| < 256),
 // so only the summation order differs from the reference.  With groups, the MFMAs of a group
 // accumulate into a second set of registers that is folded into the total with the group's
-// scales (acc += accg * s[g]) at the group's last block.
+// scales (acc += accg * s[g]) at the group's last block; to leave room for that set, a grouped
+// workgroup's tile is 256 x 64, each wave keeping two of the four interleaved column sets
+// (columns 4*cg + 2*wc + c of the Bt tile, read with the same swizzles).
 //
 // Tiling.  A workgroup (8 waves, two per SIMD) computes a 256 x 128 output tile; wave w owns
 // rows [64 wr, 64 wr + 64) x columns [64 wc, 64 wc + 64) with wr = w % 4, wc = w / 4.  K advances
@@ -21,8 +23,8 @@
 //     and its 16-byte k-chunks are XOR-swizzled by (p >> 3) & 7: the 16 lanes of a B-operand read
 //     (columns 4 apart) then cover both halves of the banks and 8 distinct chunks in each.
 // Block kb runs its MFMAs from buffer kb % 2 while the workgroup's loads of block kb + 4 travel
-// into registers (four blocks of lead cover an L2 miss; two with scale groups, whose second
-// accumulator set takes the registers) and block kb + 1, loaded earlier, is written into the
+// into registers (four blocks of lead cover an L2 miss) and block kb + 1, loaded earlier, is
+// written into the
 // other buffer: each thread loads 4 x 16 bytes of x (8 threads per 128-byte row segment) and
 // 4 rows x 4 columns of 8-bit weights (32 threads per 128-byte row segment) or 2 rows x 8
 // columns of 4-bit weights (16 threads per 64-byte row segment) per block.  One barrier per block publishes the next buffers and retires the reads
@@ -58,7 +60,7 @@ constexpr int kLds = 2 * kABytes + 2 * kBtBytes;
 constexpr int kXLoads = kABytes / (kThreads * 16);  // 16-byte x loads per thread per block
 constexpr int kWLoads = 4;                           // w loads (4 bytes) per thread per block
 constexpr int kPf = 4;                               // blocks loaded ahead into registers
-constexpr int kPfGrouped = 2;                        // the same with scale groups
+constexpr int kPfGrouped = 4;                        // the same with scale groups
 constexpr int kUnroll = 4;                           // multiple of kPf and of the 2 LDS buffers
 static_assert(kXLoads * kThreads * 16 == kABytes, "x load split");
 static_assert(kBK * kBN == 16 * kThreads, "conversion: 16 weights per thread");
@@ -136,6 +138,11 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
 template <int BK, bool GRP>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   constexpr int PF = GRP ? kPfGrouped : kPf;
+  // With scale groups the tile is 256 x 64: each wave keeps two of the four interleaved MFMA
+  // column sets (columns 4*cg + 2*wc + c, c = 0, 1), which halves both accumulator sets so that
+  // the second one fits beside the operands without spilling.
+  constexpr int BN = GRP ? kBN / 2 : kBN;
+  constexpr int NC = GRP ? 2 : 4;  // MFMA column sets per wave
   static_assert(kUnroll % PF == 0, "register slots cycle within the unroll");
   // Tile order: consecutive work items go to one XCD (workgroups are dispatched round-robin over
   // the 8); with whole 2 x 16 tile groups, 32 consecutive items form one group.  DotGeneral
@@ -159,7 +166,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     tm = item / a.tiles_n;
     tn = item % a.tiles_n;
   }
-  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int m0 = tm * kBM, n0 = tn * BN;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wr = wave & 3, wc = wave >> 2;
   const int cg = lane & 15, kq = lane >> 4;
@@ -198,7 +205,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // 4-bit kinds: thread t converts columns 8*cq .. 8*cq + 7 and rows 2*j, 2*j + 1 of each block
   // (cq = t % 16, j = t / 16); the 16 threads of a j read one 64-byte row segment.
   constexpr int kEB = kDotB<BK> ? 2 : 1;  // bytes per B element
-  const int cq = k4B<BK> ? (t & 15) : (t & 31), j = k4B<BK> ? (t >> 4) : (t >> 5);
+  // Threads per row group of the B tile; with the 64-column tile the second half of the threads
+  // repeats the first half's rows (their loads hit the cache and they store nothing).
+  constexpr int kCQ = (k4B<BK> ? 16 : 32) * BN / kBN;
+  constexpr int kJ = kThreads * BN / kBN / kCQ;  // row groups of one block
+  const int cq = t % kCQ, jt = t / kCQ, j = jt % kJ;
+  const bool b_store = jt < kJ;
   const int cpt = k4B<BK> ? 8 : 4;  // columns per thread
   const int wcol = n0 + cpt * cq + cpt <= a.N ? n0 + cpt * cq : 0;
   const uint8_t* wsrc = k4B<BK> ? a.w + ((size_t)(2 * j) * N + wcol) / 2 : a.w + ((size_t)(4 * j) * N + wcol) * kEB;
@@ -250,6 +262,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // Four k-values of each of four consecutive columns (Bt rows 128 bytes apart): int8 converted
   // exactly to bf16, half values regrouped by column.  [N, K]: the chunks as loaded.
   auto store_w = [&](const uint32_t (&w4)[kWWords], int buf) {
+    if (GRP && !b_store) return;
     if constexpr (k4B<BK>) {
       // Nibble c of each row word is column 8*cq + c (reference packing: low nibble first);
       // both rows converted exactly through f32 and packed as a bf16 pair.
@@ -297,41 +310,45 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   };
 
   // acc: the total; accg: the current scale group's sums (grouped scales only).
-  f32x4_t acc[4][4], accg[4][4];
+  f32x4_t acc[4][NC], accg[4][NC];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[rb][c] = accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < NC; ++c) acc[rb][c] = accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // Grouped scales: this lane's 4 columns' scales of the group being summed, loaded a group ahead.
-  const int scol = min(n0 + 64 * wc + 4 * cg, a.N - 4);
-  float sg[4] = {0.f, 0.f, 0.f, 0.f};
+  // This lane's first column: 64*wc + 4*cg (four consecutive), or 4*cg + 2*wc (two) with groups.
+  const int lcol = GRP ? n0 + 4 * cg + 2 * wc : n0 + 64 * wc + 4 * cg;
+  const int scol = min(lcol, a.N - NC);
+  float sg[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) sg[c] = 0.f;
   auto load_sg = [&](int g) __attribute__((always_inline)) {
     g = min(g, a.K / (kBK * max(a.gpb, 1)) - 1);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) sg[c] = load_f(a.scale, (size_t)g * N + scol + c, a.s_dt);
+    for (int c = 0; c < NC; ++c) sg[c] = load_f(a.scale, (size_t)g * N + scol + c, a.s_dt);
   };
   if constexpr (GRP) load_sg(0);
 
   // MFMA operands of one 32-row step: x row 64*wr + 16*rb + cg, Bt column 64*wc + 4*cg + c (Bt
-  // row 64*wc + 4*cg + (c ^ (cg & 1))).
+  // row 64*wc + 4*cg + (c ^ (cg & 1))); with groups, Bt column 4*cg + 2*wc + c.
   const uint32_t a_row = (uint32_t)((64 * wr + cg) * (kBK * 2));
-  const uint32_t b_col = (uint32_t)((64 * wc + 4 * cg) * (kBK * 2));
-  const int b_par = cg & 1;
+  const uint32_t b_col = (uint32_t)(((GRP ? 0 : 64 * wc) + 4 * cg) * (kBK * 2));
+  const int b_par = cg & 1, c_base = GRP ? 2 * wc : 0;
   // Operands of one 32-row step (sub = 0, 1 of a block) from LDS buffer buf, and its 16 MFMAs.
-  auto read_step = [&](int buf, int sub, u32x4_v (&A)[4], u32x4_v (&B)[4]) {
+  auto read_step = [&](int buf, int sub, u32x4_v (&A)[4], u32x4_v (&B)[NC]) {
     const int kc = 4 * sub + kq;  // 16-byte k-chunk of this lane
     const uint8_t* ap = &xs[buf][a_row + ((kc ^ (cg >> 1)) << 4)];
     const uint8_t* bp = &bt[buf][b_col + ((kc ^ ((cg >> 1) & 7)) << 4)];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) A[rb] = *(const u32x4_v*)(ap + rb * 16 * (kBK * 2));
 #pragma unroll
-    for (int c = 0; c < 4; ++c) B[c] = *(const u32x4_v*)(bp + (c ^ b_par) * (kBK * 2));
+    for (int c = 0; c < NC; ++c) B[c] = *(const u32x4_v*)(bp + ((c_base + c) ^ b_par) * (kBK * 2));
   };
-  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[4]) __attribute__((always_inline)) {
+  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[NC]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < NC; ++c) {
         if constexpr (GRP)
           accg[rb][c] = mfma<BK>(A[rb], B[c], accg[rb][c]);
         else
@@ -343,7 +360,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < NC; ++c) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[rb][c][r] = __builtin_fmaf(accg[rb][c][r], sg[c], acc[rb][c][r]);
         accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -360,7 +377,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // (sched_barrier keeps the compiler from regrouping the phases.)
   u32x4_v xr[PF][kXLoads];
   uint32_t wr4[PF][kWWords];
-  u32x4_v A0[4], B0[4], A1[4], B1[4];
+  u32x4_v A0[4], B0[NC], A1[4], B1[NC];
   auto block = [&](int kb, auto step) __attribute__((always_inline)) {
     constexpr int U = decltype(step)::value;  // kb % kUnroll
     constexpr int S = U % PF, S1 = (U + 1) % PF, B = U % 2;
@@ -372,12 +389,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     store_w(wr4[S1], B ^ 1);
     mma_step(A0, B0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 2 * NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 2 * NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
       __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -391,12 +408,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     load_w(kb + PF, wr4[S]);
     mma_step(A1, B1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 2 * NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 2 * NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
@@ -427,7 +444,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 
   // Epilogue: y = act(acc * s[n] + bias[n]) for this lane's 4 columns (DotGeneral: the f32 sums,
   // or the sums rounded to the half output dtype as ConvertDType rounds them, 4 columns per store).
-  const int ncol = n0 + 64 * wc + 4 * cg;
+  const int ncol = lcol;
   if (ncol >= a.N) return;
   if constexpr (kDotB<BK>) {
     const int r0 = m0 + 64 * wr + 4 * kq;
@@ -449,6 +466,33 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
         }
       }
     return;
+  } else if constexpr (GRP) {
+    // Two consecutive columns per row (the scales were applied by fold()): bias, activation, bf16.
+    float bi[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) bi[c] = a.bias ? load_f(a.bias, ncol + c, a.b_dt) : 0.0f;
+    const int row0 = m0 + 64 * wr + 4 * kq;
+    uint16_t* out = (uint16_t*)a.out;
+    auto store2 = [&](auto actc) __attribute__((always_inline)) {
+      constexpr int ACT = decltype(actc)::value;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = row0 + 16 * rb + r;
+          if (row < a.M)
+            *(uint32_t*)(out + (size_t)row * N + ncol) =
+                scaled_act_bf16x2<ACT>(acc[rb][0][r], 1.0f, bi[0], acc[rb][1][r], 1.0f, bi[1]);
+        }
+    };
+    switch (a.act) {
+      case MX_ACT_GELU: store2(std::integral_constant<int, MX_ACT_GELU>{}); break;
+      case MX_ACT_RELU: store2(std::integral_constant<int, MX_ACT_RELU>{}); break;
+      case MX_ACT_SILU: store2(std::integral_constant<int, MX_ACT_SILU>{}); break;
+      case MX_ACT_HARDSWISH: store2(std::integral_constant<int, MX_ACT_HARDSWISH>{}); break;
+      case MX_ACT_TANH: store2(std::integral_constant<int, MX_ACT_TANH>{}); break;
+      default: store2(std::integral_constant<int, MX_ACT_NONE>{}); break;
+    }
   } else {
   float sc[4], bi[4];
 #pragma unroll
@@ -496,13 +540,14 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.s_dt = d.s_dt;
   ga.b_dt = d.b_dt;
   ga.act = d.act;
-  const int64_t tiles_m = (d.M + kBM - 1) / kBM, tiles_n = (d.N + kBN - 1) / kBN;
+  const bool grouped = d.block_size < d.K;
+  const int64_t bn = grouped ? kBN / 2 : kBN;  // the kernel's tile width (64 with scale groups)
+  const int64_t tiles_m = (d.M + kBM - 1) / kBM, tiles_n = (d.N + bn - 1) / bn;
   if (tiles_m * tiles_n > (int64_t)1 << 30)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: output too large for the GEMM path");
   ga.tiles_n = (int)tiles_n;
   ga.grouped = (tiles_m % 2 == 0 && tiles_n % 16 == 0) ? 1 : 0;
   ga.tiles = (int)(tiles_m * tiles_n);
-  const bool grouped = d.block_size < d.K;
   ga.gpb = grouped ? (int)(d.block_size / kBK) : 0;
   const int grid = (int)(tiles_m * tiles_n);
   hipStream_t st = b->stream;
