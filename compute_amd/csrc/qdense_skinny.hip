@@ -140,12 +140,11 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
   __shared__ int s_last;
 
   const int item = sk_xcd_swizzle(blockIdx.x, gridDim.x);
-  // Work items of a column block are consecutive: [matrix (pair mode)][slice].
-  const int SP = a.pair ? 2 * a.S : a.S;  // partial tiles per column block
-  const int cb = item / SP, part = item % SP;
-  const int mat = part >= a.S ? 1 : 0, slice = part - mat * a.S;
-  const uint8_t* wmat = mat ? a.w2 : a.w;
-  const void* smat = mat ? a.scale2 : a.scale;
+  // Work items of a column block are consecutive slices.  In pair mode a workgroup computes its
+  // slice of both products, one after the other, each summed exactly as its own launch sums it.
+  const int NM = a.pair ? 2 : 1;
+  const int SP = NM * a.S;  // partial tiles per column block, [matrix][slice]
+  const int cb = item / a.S, slice = item % a.S;
   // The wave index is wave-uniform; saying so keeps the control flow scalar.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int cg = lane & 15, kq = lane >> 4;
@@ -154,168 +153,191 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
   const int cblk = cb * kCols;
   const int col0 = cblk + cg * CPL;
 
-  float tot[CPL][MR];
+  const int M = a.M;
+  constexpr int kQPR = kCols / 4;  // quads per tile row
+  constexpr int kMaxQ = kSkMaxRows * kQPR / kSkThreads;  // quads per thread (M = 16)
+  const int t = threadIdx.x;
+  const int MC = M * kCols, NQ = M * kQPR;
+  auto wave_sum = [&](int g) __attribute__((always_inline)) {
+    f32x4_t y = *(const f32x4_t*)(red + 4 * g);
 #pragma unroll
-  for (int c = 0; c < CPL; ++c)
-#pragma unroll
-    for (int r = 0; r < MR; ++r) tot[c][r] = 0.0f;
-
-  if (k0 < KS) {
-    // Lanes whose columns lie past N read column 0 instead (their results are never stored).
-    const size_t row_bytes = kI4 ? (size_t)(a.N >> 1) : (size_t)a.N;
-    const size_t lbyte = kI4 ? (size_t)(col0 >> 1) : (size_t)col0;
-    const uint8_t* wp = wmat + (size_t)(8 * kq) * row_bytes + (lbyte + kSkLaneBytes <= row_bytes ? lbyte : 0);
-    const uint16_t* xp = a.x + (size_t)min(cg, a.M - 1) * a.K + 8 * kq;
-    const char* sp = (const char*)smat + (size_t)(col0 < a.N ? col0 : 0) * (SF32 ? 4 : 2);
-    const size_t srow = (size_t)a.N * (SF32 ? 4 : 2);
-
-    // One step's operands: x (16 bytes), eight 8-byte weight row segments, and the scales of the
-    // step's group (loaded with every step, so that every step issues the same loads and each
-    // wait is exact; the repeats within a group hit the cache).
-    struct Slot {
-      u32x4_v x;
-      u32x2_v w[8];
-      u32x4_v s[kSLoads];
-    };
-    int ig = k0 / a.FS, irem = a.FS - k0 % a.FS;  // group and steps left in it, issue order
-    auto issue = [&](Slot& sl, int k) __attribute__((always_inline)) {
-      sl.x = *(const u32x4_v*)(xp + 32 * k);
-      const uint8_t* wk = wp + (size_t)(32 * k) * row_bytes;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sl.w[e] = __builtin_nontemporal_load((const u32x2_v*)(wk + (size_t)e * row_bytes));
-      const char* sg = sp + (size_t)ig * srow;
-#pragma unroll
-      for (int q = 0; q < kSLoads; ++q) sl.s[q] = *(const u32x4_v*)(sg + 16 * q);
-      if (--irem == 0) {
-        ++ig;
-        irem = a.FS;
-      }
-    };
-
-    // A nibble u (bits 0-3 and 16-19 after the mask) becomes the bf16 pattern 0x4300 | u =
-    // 128 + u with one xor (the mask leaves no other bits); for Int4 the same xor also flips bit 3
-    // of the nibble, giving 136 + w.  (x & m) ^ c is one v_bitop3_b32.
-    const uint32_t kMask = 0x000F000Fu;
-    const uint32_t kOr = vgpr_const(WDT == MX_DTYPE_INT4 ? 0x43084308u : 0x43004300u);
-    const u32x4_v ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-    const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4_t grp[CPL], sx = zero;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) grp[c] = zero;
-    // A step: dequantise into MFMA B operands and accumulate the group's partial sums.
-    auto compute = [&](const Slot& sl) __attribute__((always_inline)) {
-      if constexpr (kI4) {
-#pragma unroll
-        for (int d = 0; d < CPL / 8; ++d) {
-          uint32_t bq[8][4];  // columns 8d + 0..7, four pair-dwords each
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t A = sl.w[2 * pp][d], B = sl.w[2 * pp + 1][d];
-            const uint32_t t0 = __builtin_amdgcn_perm(B, A, 0x06040200u);  // [A.b0, A.b2, B.b0, B.b2]
-            const uint32_t t1 = __builtin_amdgcn_perm(B, A, 0x07050301u);  // [A.b1, A.b3, B.b1, B.b3]
-            bq[0][pp] = (t0 & kMask) ^ kOr;
-            bq[1][pp] = ((t0 >> 4) & kMask) ^ kOr;
-            bq[4][pp] = ((t0 >> 8) & kMask) ^ kOr;
-            bq[5][pp] = ((t0 >> 12) & kMask) ^ kOr;
-            bq[2][pp] = (t1 & kMask) ^ kOr;
-            bq[3][pp] = ((t1 >> 4) & kMask) ^ kOr;
-            bq[6][pp] = ((t1 >> 8) & kMask) ^ kOr;
-            bq[7][pp] = ((t1 >> 12) & kMask) ^ kOr;
-          }
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-            grp[8 * d + c] = sk_mfma(sl.x, u32x4_v{bq[c][0], bq[c][1], bq[c][2], bq[c][3]}, grp[8 * d + c]);
-        }
-        sx = sk_mfma(sl.x, ones, sx);
-      } else {
-#pragma unroll
-        for (int d = 0; d < CPL / 4; ++d) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            uint32_t bq[4];
-#pragma unroll
-            for (int pp = 0; pp < 4; ++pp) {
-              const uint32_t r0 = sl.w[2 * pp][d], r1 = sl.w[2 * pp + 1][d];
-              float f0, f1;
-              if constexpr (WDT == MX_DTYPE_INT8) {
-                f0 = (float)(int8_t)(r0 >> (8 * c));
-                f1 = (float)(int8_t)(r1 >> (8 * c));
-              } else {
-                f0 = (float)(uint8_t)(r0 >> (8 * c));
-                f1 = (float)(uint8_t)(r1 >> (8 * c));
-              }
-              bq[pp] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-            }
-            grp[4 * d + c] = sk_mfma(sl.x, u32x4_v{bq[0], bq[1], bq[2], bq[3]}, grp[4 * d + c]);
-          }
-        }
-      }
-    };
-    // The group's scale, once per group (or at the end of the wave's steps):
-    // tot += (grp - offset * rowsum(x)) * s, then the group sums start again from zero.
-    auto fold = [&](const Slot& sl) __attribute__((always_inline)) {
-      float sc[CPL];
-      if constexpr (SF32) {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) sc[c] = __uint_as_float(sl.s[c / 4][c % 4]);
-      } else {
-#pragma unroll
-        for (int c = 0; c < CPL; c += 2) {
-          const uint32_t v = sl.s[c / 8][(c / 2) % 4];
-          sc[c] = __uint_as_float(v << 16);
-          sc[c + 1] = __uint_as_float(v & 0xFFFF0000u);
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < CPL; ++c)
-#pragma unroll
-        for (int r = 0; r < MR; ++r)
-          tot[c][r] = __builtin_fmaf(kOff != 0.0f ? grp[c][r] - kOff * sx[r] : grp[c][r], sc[c], tot[c][r]);
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) grp[c] = zero;
-      sx = zero;
-    };
-    int crem = a.FS - k0 % a.FS;  // steps left in the current group, compute order
-    auto step = [&](const Slot& sl, int t) __attribute__((always_inline)) {
-      compute(sl);
-      if (--crem == 0 || t == a.T - 1) {
-        fold(sl);
-        if (crem == 0) crem = a.FS;
-      }
-    };
-
-    if constexpr (PIPE) {
-      // Two slots: step t + 2 is issued into a slot as soon as step t has used it, so each
-      // wave keeps two steps of loads in flight while it computes.  The last two steps are
-      // peeled off the loop so that every loop iteration issues the same loads.
-      Slot A, B;
-      issue(A, k0);
-      issue(B, k0 + 1);
-      __builtin_amdgcn_sched_barrier(0);
-      int t = 0;
+    for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
+    return y;
+  };
+  // The workgroup's tile of each product, summed over the waves (quad g = t + i * kSkThreads):
+  // the last product's stays as the waves' tiles in LDS, the first of a pair is summed into an
+  // LDS tile of its own before the second is computed.
+  float* held = red + (size_t)kSkWaves * M * kCols;
+  auto tile = [&](int mat, int i) __attribute__((always_inline)) {
+    const int g = min(t + i * kSkThreads, NQ - 1);
+    return mat + 1 < NM ? *(const f32x4_t*)(held + 4 * g) : wave_sum(g);
+  };
 #pragma unroll 1
-      for (; t < a.T - 2; t += 2) {
+  for (int mat = 0; mat < NM; ++mat) {
+  const uint8_t* wmat = mat ? a.w2 : a.w;
+  const void* smat = mat ? a.scale2 : a.scale;
+  float tot[CPL][MR];
+  #pragma unroll
+    for (int c = 0; c < CPL; ++c)
+  #pragma unroll
+      for (int r = 0; r < MR; ++r) tot[c][r] = 0.0f;
+  
+    if (k0 < KS) {
+      // Lanes whose columns lie past N read column 0 instead (their results are never stored).
+      const size_t row_bytes = kI4 ? (size_t)(a.N >> 1) : (size_t)a.N;
+      const size_t lbyte = kI4 ? (size_t)(col0 >> 1) : (size_t)col0;
+      const uint8_t* wp = wmat + (size_t)(8 * kq) * row_bytes + (lbyte + kSkLaneBytes <= row_bytes ? lbyte : 0);
+      const uint16_t* xp = a.x + (size_t)min(cg, a.M - 1) * a.K + 8 * kq;
+      const char* sp = (const char*)smat + (size_t)(col0 < a.N ? col0 : 0) * (SF32 ? 4 : 2);
+      const size_t srow = (size_t)a.N * (SF32 ? 4 : 2);
+  
+      // One step's operands: x (16 bytes), eight 8-byte weight row segments, and the scales of the
+      // step's group (loaded with every step, so that every step issues the same loads and each
+      // wait is exact; the repeats within a group hit the cache).
+      struct Slot {
+        u32x4_v x;
+        u32x2_v w[8];
+        u32x4_v s[kSLoads];
+      };
+      int ig = k0 / a.FS, irem = a.FS - k0 % a.FS;  // group and steps left in it, issue order
+      auto issue = [&](Slot& sl, int k) __attribute__((always_inline)) {
+        sl.x = *(const u32x4_v*)(xp + 32 * k);
+        const uint8_t* wk = wp + (size_t)(32 * k) * row_bytes;
+  #pragma unroll
+        for (int e = 0; e < 8; ++e) sl.w[e] = __builtin_nontemporal_load((const u32x2_v*)(wk + (size_t)e * row_bytes));
+        const char* sg = sp + (size_t)ig * srow;
+  #pragma unroll
+        for (int q = 0; q < kSLoads; ++q) sl.s[q] = *(const u32x4_v*)(sg + 16 * q);
+        if (--irem == 0) {
+          ++ig;
+          irem = a.FS;
+        }
+      };
+  
+      // A nibble u (bits 0-3 and 16-19 after the mask) becomes the bf16 pattern 0x4300 | u =
+      // 128 + u with one xor (the mask leaves no other bits); for Int4 the same xor also flips bit 3
+      // of the nibble, giving 136 + w.  (x & m) ^ c is one v_bitop3_b32.
+      const uint32_t kMask = 0x000F000Fu;
+      const uint32_t kOr = vgpr_const(WDT == MX_DTYPE_INT4 ? 0x43084308u : 0x43004300u);
+      const u32x4_v ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+      const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4_t grp[CPL], sx = zero;
+  #pragma unroll
+      for (int c = 0; c < CPL; ++c) grp[c] = zero;
+      // A step: dequantise into MFMA B operands and accumulate the group's partial sums.
+      auto compute = [&](const Slot& sl) __attribute__((always_inline)) {
+        if constexpr (kI4) {
+  #pragma unroll
+          for (int d = 0; d < CPL / 8; ++d) {
+            uint32_t bq[8][4];  // columns 8d + 0..7, four pair-dwords each
+  #pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+              const uint32_t A = sl.w[2 * pp][d], B = sl.w[2 * pp + 1][d];
+              const uint32_t t0 = __builtin_amdgcn_perm(B, A, 0x06040200u);  // [A.b0, A.b2, B.b0, B.b2]
+              const uint32_t t1 = __builtin_amdgcn_perm(B, A, 0x07050301u);  // [A.b1, A.b3, B.b1, B.b3]
+              bq[0][pp] = (t0 & kMask) ^ kOr;
+              bq[1][pp] = ((t0 >> 4) & kMask) ^ kOr;
+              bq[4][pp] = ((t0 >> 8) & kMask) ^ kOr;
+              bq[5][pp] = ((t0 >> 12) & kMask) ^ kOr;
+              bq[2][pp] = (t1 & kMask) ^ kOr;
+              bq[3][pp] = ((t1 >> 4) & kMask) ^ kOr;
+              bq[6][pp] = ((t1 >> 8) & kMask) ^ kOr;
+              bq[7][pp] = ((t1 >> 12) & kMask) ^ kOr;
+            }
+  #pragma unroll
+            for (int c = 0; c < 8; ++c)
+              grp[8 * d + c] = sk_mfma(sl.x, u32x4_v{bq[c][0], bq[c][1], bq[c][2], bq[c][3]}, grp[8 * d + c]);
+          }
+          sx = sk_mfma(sl.x, ones, sx);
+        } else {
+  #pragma unroll
+          for (int d = 0; d < CPL / 4; ++d) {
+  #pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              uint32_t bq[4];
+  #pragma unroll
+              for (int pp = 0; pp < 4; ++pp) {
+                const uint32_t r0 = sl.w[2 * pp][d], r1 = sl.w[2 * pp + 1][d];
+                float f0, f1;
+                if constexpr (WDT == MX_DTYPE_INT8) {
+                  f0 = (float)(int8_t)(r0 >> (8 * c));
+                  f1 = (float)(int8_t)(r1 >> (8 * c));
+                } else {
+                  f0 = (float)(uint8_t)(r0 >> (8 * c));
+                  f1 = (float)(uint8_t)(r1 >> (8 * c));
+                }
+                bq[pp] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+              }
+              grp[4 * d + c] = sk_mfma(sl.x, u32x4_v{bq[0], bq[1], bq[2], bq[3]}, grp[4 * d + c]);
+            }
+          }
+        }
+      };
+      // The group's scale, once per group (or at the end of the wave's steps):
+      // tot += (grp - offset * rowsum(x)) * s, then the group sums start again from zero.
+      auto fold = [&](const Slot& sl) __attribute__((always_inline)) {
+        float sc[CPL];
+        if constexpr (SF32) {
+  #pragma unroll
+          for (int c = 0; c < CPL; ++c) sc[c] = __uint_as_float(sl.s[c / 4][c % 4]);
+        } else {
+  #pragma unroll
+          for (int c = 0; c < CPL; c += 2) {
+            const uint32_t v = sl.s[c / 8][(c / 2) % 4];
+            sc[c] = __uint_as_float(v << 16);
+            sc[c + 1] = __uint_as_float(v & 0xFFFF0000u);
+          }
+        }
+  #pragma unroll
+        for (int c = 0; c < CPL; ++c)
+  #pragma unroll
+          for (int r = 0; r < MR; ++r)
+            tot[c][r] = __builtin_fmaf(kOff != 0.0f ? grp[c][r] - kOff * sx[r] : grp[c][r], sc[c], tot[c][r]);
+  #pragma unroll
+        for (int c = 0; c < CPL; ++c) grp[c] = zero;
+        sx = zero;
+      };
+      int crem = a.FS - k0 % a.FS;  // steps left in the current group, compute order
+      auto step = [&](const Slot& sl, int t) __attribute__((always_inline)) {
+        compute(sl);
+        if (--crem == 0 || t == a.T - 1) {
+          fold(sl);
+          if (crem == 0) crem = a.FS;
+        }
+      };
+  
+      if constexpr (PIPE) {
+        // Two slots: step t + 2 is issued into a slot as soon as step t has used it, so each
+        // wave keeps two steps of loads in flight while it computes.  The last two steps are
+        // peeled off the loop so that every loop iteration issues the same loads.
+        Slot A, B;
+        issue(A, k0);
+        issue(B, k0 + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        int t = 0;
+  #pragma unroll 1
+        for (; t < a.T - 2; t += 2) {
+          step(A, t);
+          __builtin_amdgcn_sched_barrier(0);
+          issue(A, k0 + t + 2);
+          __builtin_amdgcn_sched_barrier(0);
+          step(B, t + 1);
+          __builtin_amdgcn_sched_barrier(0);
+          issue(B, k0 + t + 3);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         step(A, t);
-        __builtin_amdgcn_sched_barrier(0);
-        issue(A, k0 + t + 2);
-        __builtin_amdgcn_sched_barrier(0);
         step(B, t + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        issue(B, k0 + t + 3);
-        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        Slot A;
+        issue(A, k0);
+        step(A, 0);
       }
-      step(A, t);
-      step(B, t + 1);
-    } else {
-      Slot A;
-      issue(A, k0);
-      step(A, 0);
     }
-  }
+  
 
   // Every wave's tile (rows < M) into LDS as [waves][M][kCols]; each output then adds the waves
   // in a fixed order.  Outputs are handled in quads (4 consecutive columns of one row).
-  const int M = a.M;
   {
     float* rw = red + (size_t)wave * M * kCols;
 #pragma unroll
@@ -329,36 +351,41 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
     }
   }
   __syncthreads();
-  constexpr int kQPR = kCols / 4;  // quads per tile row
-  const int t = threadIdx.x;
-  const int MC = M * kCols, NQ = M * kQPR;
-  auto wave_sum = [&](int g) __attribute__((always_inline)) {
-    f32x4_t y = *(const f32x4_t*)(red + 4 * g);
+  if (mat + 1 < NM) {
 #pragma unroll
-    for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
-    return y;
-  };
+    for (int i = 0; i < kMaxQ; ++i) {
+      const int g = min(t + i * kSkThreads, NQ - 1);
+      *(f32x4_t*)(held + 4 * g) = wave_sum(g);
+    }
+    __syncthreads();  // the waves' tiles are free for the next product
+  }
+  }
 
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
       a.partial, (short)0, (int)((size_t)SP * M * a.N * sizeof(float)), 0x00020000);
   constexpr int kSc1 = 16;  // cache-policy operand of the buffer intrinsics: sc1
-  if (SP > 1) {
-    // Split K (or pair mode): store this work item's tile as [matrix][slice][M][N] (16-byte
+  if (a.S > 1) {
+    // Split K: store this work item's tile of each product as [matrix][slice][M][N] (16-byte
     // stores with the agent-scope coherence bit sc1: visible across the XCDs' L2s without
     // whole-cache maintenance), wait until the stores have completed, then count the arrival.
     // Only the last arriver reads the tiles back, with loads that carry the same bit.
-#pragma unroll 1
-    for (int g = t; g < NQ; g += kSkThreads) {
+#pragma unroll
+    for (int i = 0; i < kMaxQ; ++i) {
+      const int g = t + i * kSkThreads;
       const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
-      if (col < a.N)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, wave_sum(g)), prs,
-                                              (unsigned)(((part * M + m) * a.N + col) * 4), 0, kSc1);
+      if (g < NQ && col < a.N) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, tile(0, i)), prs,
+                                              (unsigned)(((slice * M + m) * a.N + col) * 4), 0, kSc1);
+        if (a.pair)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, tile(1, i)), prs,
+                                                (unsigned)((((a.S + slice) * M + m) * a.N + col) * 4), 0, kSc1);
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
       const uint32_t prev = __hip_atomic_fetch_add(&a.counters[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = prev == (uint32_t)SP - 1u;
+      const int last = prev == (uint32_t)a.S - 1u;  // one arrival per slice
       if (last) __hip_atomic_store(&a.counters[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_last = last;
     }
@@ -375,13 +402,15 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
   constexpr int kSl = 8;  // partial tiles per batch of loads (all in flight together)
   const bool plain = a.act == MX_ACT_NONE && !a.pair && !a.res_op;
 #pragma unroll 1
-  for (int g = t; g < NQ; g += kSkThreads) {
+  for (int i = 0; i < kMaxQ; ++i) {
+    const int g = t + i * kSkThreads;
     const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
-    if (col >= a.N) continue;
+    if (g >= NQ || col >= a.N) continue;
     f32x4_t y, y2;
-    if (SP == 1) {
-      y = wave_sum(g);
-      y2 = y;
+    if (a.S == 1) {
+      // This workgroup holds every tile of the column block.
+      y = tile(0, i);
+      y2 = a.pair ? tile(1, i) : y;
     } else {
       y = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       y2 = y;
@@ -546,9 +575,9 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.pair = d.pair ? 1 : 0;
   ga.act2 = d.act2;
   ga.b2_dt = d.b2_dt;
-  const int grid = (int)(nb * SP);
-  // LDS: the waves' tiles [waves][M][cols].
-  const size_t lds = (size_t)kSkWaves * d.M * cols * sizeof(float);
+  const int grid = (int)(nb * S);
+  // LDS: the waves' tiles [waves][M][cols] and the first product's tile [M][cols].
+  const size_t lds = (size_t)(kSkWaves + 1) * d.M * cols * sizeof(float);
   const bool sf32 = d.s_dt == MX_DTYPE_FLOAT32;
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
