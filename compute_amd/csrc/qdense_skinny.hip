@@ -47,6 +47,7 @@
 // slice order (deterministic), adds the bias, applies the activation and rounds to bf16.
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "device_common.h"
 #include "mxrt_internal.h"
@@ -129,7 +130,9 @@ __device__ __forceinline__ float sk_value(SkWord v, const void* p, int dt) {
 // T == 1).  The main loop is a rolled loop whose body is two steps, so the code a CU fetches
 // stays small: a kernel this short-lived runs its instructions cold, and every instruction-cache
 // line it misses costs a trip to L2 or beyond.
-template <int WDT, int MR, bool SF32, bool PIPE>
+// G2: the scale groups are two steps (G = 64), so a group is exactly one loop iteration's pair:
+// its first step's MFMAs start from zero and its second folds, with no clearing of the sums.
+template <int WDT, int MR, bool SF32, bool PIPE, bool G2>
 __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a) {
   constexpr bool kI4 = WDT == MX_DTYPE_INT4 || WDT == MX_DTYPE_UINT4;
   constexpr int CPL = kI4 ? 2 * kSkLaneBytes : kSkLaneBytes;  // columns per lane
@@ -225,7 +228,8 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
   #pragma unroll
       for (int c = 0; c < CPL; ++c) grp[c] = zero;
       // A step: dequantise into MFMA B operands and accumulate the group's partial sums.
-      auto compute = [&](const Slot& sl) __attribute__((always_inline)) {
+      auto compute = [&](const Slot& sl, auto zc) __attribute__((always_inline)) {
+        constexpr bool Z = decltype(zc)::value;  // the group's first step: sums start from zero
         if constexpr (kI4) {
   #pragma unroll
           for (int d = 0; d < CPL / 8; ++d) {
@@ -246,9 +250,9 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
             }
   #pragma unroll
             for (int c = 0; c < 8; ++c)
-              grp[8 * d + c] = sk_mfma(sl.x, u32x4_v{bq[c][0], bq[c][1], bq[c][2], bq[c][3]}, grp[8 * d + c]);
+              grp[8 * d + c] = sk_mfma(sl.x, u32x4_v{bq[c][0], bq[c][1], bq[c][2], bq[c][3]}, Z ? zero : grp[8 * d + c]);
           }
-          sx = sk_mfma(sl.x, ones, sx);
+          sx = sk_mfma(sl.x, ones, Z ? zero : sx);
         } else {
   #pragma unroll
           for (int d = 0; d < CPL / 4; ++d) {
@@ -268,14 +272,14 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
                 }
                 bq[pp] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
               }
-              grp[4 * d + c] = sk_mfma(sl.x, u32x4_v{bq[0], bq[1], bq[2], bq[3]}, grp[4 * d + c]);
+              grp[4 * d + c] = sk_mfma(sl.x, u32x4_v{bq[0], bq[1], bq[2], bq[3]}, Z ? zero : grp[4 * d + c]);
             }
           }
         }
       };
       // The group's scale, once per group (or at the end of the wave's steps):
       // tot += (grp - offset * rowsum(x)) * s, then the group sums start again from zero.
-      auto fold = [&](const Slot& sl) __attribute__((always_inline)) {
+      auto fold = [&](const Slot& sl, auto zr) __attribute__((always_inline)) {
         float sc[CPL];
         if constexpr (SF32) {
   #pragma unroll
@@ -293,16 +297,31 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
   #pragma unroll
           for (int r = 0; r < MR; ++r)
             tot[c][r] = __builtin_fmaf(kOff != 0.0f ? grp[c][r] - kOff * sx[r] : grp[c][r], sc[c], tot[c][r]);
+        if constexpr (decltype(zr)::value) {  // the next group's sums start from zero
   #pragma unroll
-        for (int c = 0; c < CPL; ++c) grp[c] = zero;
-        sx = zero;
+          for (int c = 0; c < CPL; ++c) grp[c] = zero;
+          sx = zero;
+        }
       };
+      using False = std::integral_constant<bool, false>;
+      using True = std::integral_constant<bool, true>;
       int crem = a.FS - k0 % a.FS;  // steps left in the current group, compute order
-      auto step = [&](const Slot& sl, int t) __attribute__((always_inline)) {
-        compute(sl);
-        if (--crem == 0 || t == a.T - 1) {
-          fold(sl);
-          if (crem == 0) crem = a.FS;
+      // odd: the parity of t, known at each call site (slot A takes even steps, slot B odd ones).
+      auto step = [&](const Slot& sl, int t, auto odd) __attribute__((always_inline)) {
+        if constexpr (G2) {
+          // Even steps open a group, odd steps close it.
+          if constexpr (!decltype(odd)::value) {
+            compute(sl, True{});
+          } else {
+            compute(sl, False{});
+            fold(sl, False{});
+          }
+        } else {
+          compute(sl, False{});
+          if (--crem == 0 || t == a.T - 1) {
+            fold(sl, True{});
+            if (crem == 0) crem = a.FS;
+          }
         }
       };
   
@@ -317,21 +336,21 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
         int t = 0;
   #pragma unroll 1
         for (; t < a.T - 2; t += 2) {
-          step(A, t);
+          step(A, t, False{});
           __builtin_amdgcn_sched_barrier(0);
           issue(A, k0 + t + 2);
           __builtin_amdgcn_sched_barrier(0);
-          step(B, t + 1);
+          step(B, t + 1, True{});
           __builtin_amdgcn_sched_barrier(0);
           issue(B, k0 + t + 3);
           __builtin_amdgcn_sched_barrier(0);
         }
-        step(A, t);
-        step(B, t + 1);
+        step(A, t, False{});
+        step(B, t + 1, True{});
       } else {
         Slot A;
         issue(A, k0);
-        step(A, 0);
+        step(A, 0, False{});
       }
     }
   
@@ -512,10 +531,12 @@ static int skinny_steps(const QDenseDesc& d, int64_t nb, int num_cus) {
 
 template <int WDT, int MR, bool SF32>
 static void launch_pipe(const SkinnyArgs& ga, int grid, size_t lds, hipStream_t st) {
-  if (ga.T >= 2)
-    dispatch(qdense_skinny_kernel<WDT, MR, SF32, true>, grid, kSkThreads, lds, st, ga);
+  if (ga.T >= 2 && ga.FS == 2)
+    dispatch(qdense_skinny_kernel<WDT, MR, SF32, true, true>, grid, kSkThreads, lds, st, ga);
+  else if (ga.T >= 2)
+    dispatch(qdense_skinny_kernel<WDT, MR, SF32, true, false>, grid, kSkThreads, lds, st, ga);
   else
-    dispatch(qdense_skinny_kernel<WDT, MR, SF32, false>, grid, kSkThreads, lds, st, ga);
+    dispatch(qdense_skinny_kernel<WDT, MR, SF32, false, false>, grid, kSkThreads, lds, st, ga);
 }
 
 template <int WDT>
