@@ -246,7 +246,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--extra", default="C3,C4,C5,Q1,Q2,G1,G2,R1,R3,D1", help="comma list of other configs to report under 'extra'")
+    ap.add_argument("--extra", default="C1,C3,C4,C5,Q1,Q2,G1,G2,R1,R3,D1",
+                    help="comma list of other configs to report under 'extra' (C1's wall time per call, with a "
+                         "kernel of a few microseconds, bounds the host time of one Execute)")
     ap.add_argument("--only", default="", help="run only this config (profiling passes); prints its entry")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-crossover", dest="crossover", action="store_false",
