@@ -21,6 +21,7 @@
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "device_common.h"
 #include "mxrt_internal.h"
@@ -111,43 +112,225 @@ int qdense_validate(const mx_qdense_args* a, QDenseDesc* d) {
 }
 
 // =============================================================================================
-// Reference-order kernel.
+// Reference-order kernel: every output is summed exactly as the reference loop sums it (bias
+// first, then k in increasing order, each product and sum rounded on its own), so the result is
+// bit-identical.  That order is a chain per output; the kernel keeps the chain fed instead of
+// waiting on memory at every k:
+//   - a thread computes R rows of one column (R = 8 amortises the weight decoding when the grid
+//     has waves to spare, R = 1 spreads a small problem over more waves);
+//   - the workgroup's rows of x are staged in LDS, kExactKC values per row at a time;
+//   - the weights and scales of a batch of consecutive k (16 or 64) are requested as raw bytes/bits one batch
+//     ahead (two register slots), and decoded only when they are used.
 // =============================================================================================
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kExactThreads = 256;
-constexpr int kExactRows = 8;  // rows of x per thread (weights decoded once per k for all of them)
+constexpr int kExactKC = 512;  // x values per row staged in LDS at a time
+constexpr int kExactU = 16;    // k per batch of weight / scale requests (see U)
 
+// Branch-free operand access for the reference-order loop (the dtypes are run-time values, and a
+// branch per dtype per k would make the unrolled loop too large for the instruction cache):
+//   - weight element i lives in byte i / 2 (4-bit kinds: nibble i % 2) or byte i, and is one
+//     signed or unsigned bit-field extract of that byte;
+//   - a bf16 or f32 element (scales, zero points) is read as the aligned 32-bit word holding it
+//     and shifted into f32 position (bf16 widened exactly).
+// Element indices advance by a constant per k: no multiplication or division per k.
+__device__ __forceinline__ uint32_t word_of(const void* p, uint64_t i, int sh) {
+  return *(const uint32_t*)((const char*)p + ((i << sh) & ~(uint64_t)3));
+}
+// The f32 value of element i from its word: f32 (sh 2) as is, bf16 (sh 1) moved to the high half.
+__device__ __forceinline__ uint32_t word_shift(uint64_t i, int sh) { return sh == 2 || (i & 1) ? 0u : 16u; }
+__device__ __forceinline__ float word_value(uint32_t w, uint32_t shift, uint32_t mask) {
+  return __uint_as_float((w << shift) & mask);
+}
+
+// R: rows per thread.  ZP: zero points.  SK: the scale varies along K (groups or the reference
+// layout); else one scale per column, loaded once.
+template <int R, bool ZP, bool SK>
 __global__ __launch_bounds__(kExactThreads) void qdense_exact_kernel(QDenseDesc d) {
-  const int64_t n = (int64_t)blockIdx.x * kExactThreads + threadIdx.x;
-  const int64_t m0 = (int64_t)blockIdx.y * kExactRows;
-  if (n >= d.N) return;
+  // k per batch of requests: 64 when a thread has one row and one scale per column (few waves
+  // per SIMD, latency hidden only by the batch), else 16 (registers).
+  constexpr int U = R == 1 && !SK ? 64 : kExactU;
+  static_assert(kExactKC % (2 * U) == 0, "batches tile a chunk");
+  __shared__ __attribute__((aligned(16))) float xs[R][kExactKC];
+  __shared__ float nf4[16];
   const int64_t N = d.N, K = d.K, B = d.block_size;
-  const int rows = (int)min<int64_t>(kExactRows, d.M - m0);
-  float acc[kExactRows];
-  const float b0 = d.bias ? load_f(d.bias, n, d.b_dt) : 0.0f;
+  const int64_t n = (int64_t)blockIdx.x * kExactThreads + threadIdx.x;
+  const int64_t m0 = (int64_t)blockIdx.y * R;
+  const bool active = n < N;
+  const int64_t nn = active ? n : 0;  // lanes past N read column 0; their results are not stored
+  const int rows = (int)min<int64_t>(R, d.M - m0);
+  const bool packed = d.w_dt == MX_DTYPE_INT4 || d.w_dt == MX_DTYPE_UINT4;
+  const bool sgn = d.w_dt == MX_DTYPE_INT4 || d.w_dt == MX_DTYPE_INT8;
+  const uint32_t wbits = packed ? 4u : 8u, wsh = packed ? 1u : 0u;
+  const int s_sh = d.s_dt == MX_DTYPE_BFLOAT16 ? 1 : 2, z_sh = d.zp_dt == MX_DTYPE_BFLOAT16 ? 1 : 2;
+  const uint32_t s_mask = s_sh == 2 ? ~0u : 0xFFFF0000u, z_mask = z_sh == 2 ? ~0u : 0xFFFF0000u;
+  const bool nf = d.scheme == MX_QUANT_NF4;
+  if (threadIdx.x < 16) nf4[threadIdx.x] = kNF4Table[threadIdx.x];
+  // Scale (and zero point) of row k: block_axis 1 (reference layout, [K, ceil(N/B)]) at
+  // k * nb + n / B, stepping by nb; block_axis 0 ([ceil(K/B), N]) at (k / B) * N + n, stepping by
+  // N at each group's end.
+  const bool ax1 = d.block_axis == 1;
+  const int64_t nb = (N + B - 1) / B;
+  const int64_t scol = ax1 ? (int64_t)((uint32_t)nn / (uint32_t)B) : nn;
+  float s_col = 0.0f, z_col = 0.0f;  // one scale per column (SK false)
+  if constexpr (!SK) {
+    s_col = word_value(word_of(d.scale, (uint64_t)scol, s_sh), word_shift((uint64_t)scol, s_sh), s_mask);
+    if constexpr (ZP) z_col = word_value(word_of(d.zp, (uint64_t)scol, z_sh), word_shift((uint64_t)scol, z_sh), z_mask);
+  }
+  float acc[R];
+  const float b0 = d.bias ? load_f(d.bias, nn, d.b_dt) : 0.0f;
 #pragma unroll
-  for (int r = 0; r < kExactRows; ++r) acc[r] = b0;
-  const int64_t nb = (N + B - 1) / B;  // reference layout: scale [K, ceil(N/B)]
-  for (int64_t k = 0; k < K; ++k) {
-    const int wi = decode_weight(d.w, k * N + n, d.w_dt);
-    const int64_t si = d.block_axis == 1 ? k * nb + n / B : (k / B) * N + n;
-    const float s = load_f(d.scale, si, d.s_dt);
-    const float wf = d.scheme == MX_QUANT_NF4 ? kNF4Table[(uint32_t)wi & 15u] : (float)wi;
-    if (d.zp) {
-      const float z = load_f(d.zp, si, d.zp_dt);
-      const float u = add_rn(mul_rn(wf, s), z);
-#pragma unroll
-      for (int r = 0; r < kExactRows; ++r)
-        if (r < rows) acc[r] = add_rn(acc[r], mul_rn(load_f(d.x, (m0 + r) * K + k, d.x_dt), u));
+  for (int r = 0; r < R; ++r) acc[r] = b0;
+
+  // Operands of U consecutive k as raw bytes / words, decoded when used.
+  struct Batch {
+    uint32_t w[U], s[U], z[U], ssh[U], zsh[U];
+    uint32_t off0, off1;  // bit offset of the weight in its byte at even / odd j
+  };
+  // Running element indices of the next k to request: weight k * N + n, scale / zero point.
+  uint64_t wi = 0, si = 0;
+  uint32_t gr = 0;  // block_axis 0: place of k in its group
+  auto start = [&](int k) {
+    wi = (uint64_t)k * (uint64_t)N + (uint64_t)nn;
+    if (ax1) {
+      si = (uint64_t)k * (uint64_t)nb + (uint64_t)scol;
     } else {
+      const uint32_t g = (uint32_t)k / (uint32_t)B;
+      gr = (uint32_t)k - g * (uint32_t)B;
+      si = (uint64_t)g * (uint64_t)N + (uint64_t)scol;
+    }
+  };
+  const uint32_t nodd = (uint32_t)N & 1u;
+  auto step_scale = [&]() __attribute__((always_inline)) {
+    if (ax1) {
+      si += (uint64_t)nb;
+    } else if (++gr == (uint32_t)B) {
+      gr = 0;
+      si += (uint64_t)N;
+    }
+  };
+  // Requests k0 .. k0 + U - 1 (FULL: all below kend; else those at or past kend repeat
+  // kend - 1 and are not used).
+  auto issue = [&](Batch& bt, int k0, int kend, auto fullc) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(fullc)::value;
+    // The nibble of element wi + j * N: that of wi, flipped at odd j when N is odd.
+    const uint32_t h0 = packed ? (uint32_t)wi & 1u : 0u;
+    bt.off0 = 4u * h0;
+    bt.off1 = 4u * (h0 ^ (packed ? nodd : 0u));
 #pragma unroll
-      for (int r = 0; r < kExactRows; ++r)
-        if (r < rows)
-          acc[r] = add_rn(acc[r], mul_rn(mul_rn(load_f(d.x, (m0 + r) * K + k, d.x_dt), wf), s));
+    for (int j = 0; j < U; ++j) {
+      bt.w[j] = ((const uint8_t*)d.w)[wi >> wsh];
+      if constexpr (SK) {
+        bt.s[j] = word_of(d.scale, si, s_sh);
+        bt.ssh[j] = word_shift(si, s_sh);
+        if constexpr (ZP) {
+          bt.z[j] = word_of(d.zp, si, z_sh);
+          bt.zsh[j] = word_shift(si, z_sh);
+        }
+      }
+      if (FULL || k0 + j + 1 < kend) {
+        wi += (uint64_t)N;
+        if constexpr (SK) step_scale();
+      }
+    }
+  };
+  auto compute = [&](const Batch& bt, int k0, int kend, int kc, auto fullc) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(fullc)::value;
+    // Weight values of the batch (NF4: through the table), then the terms in k order.
+    float wf[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const uint32_t off = (j & 1) ? bt.off1 : bt.off0;
+      const int wv = sgn ? __builtin_amdgcn_sbfe((int)bt.w[j], off, wbits) : (int)__builtin_amdgcn_ubfe(bt.w[j], off, wbits);
+      wf[j] = (float)wv;
+    }
+    if (nf) {
+#pragma unroll
+      for (int j = 0; j < U; ++j) wf[j] = nf4[(uint32_t)(int)wf[j] & 15u];
+    }
+#pragma unroll
+    for (int j4 = 0; j4 < U; j4 += 4) {
+      float xv[R][4];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const f32x4_t v = *(const f32x4_t*)&xs[r][k0 + j4 - kc];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xv[r][q] = v[q];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int j = j4 + q;
+        if (FULL || k0 + j < kend) {
+          float s, z = 0.0f;
+          if constexpr (SK) {
+            s = word_value(bt.s[j], bt.ssh[j], s_mask);
+            if constexpr (ZP) z = word_value(bt.z[j], bt.zsh[j], z_mask);
+          } else {
+            s = s_col;
+            z = z_col;
+          }
+          if constexpr (ZP) {
+            const float u = add_rn(mul_rn(wf[j], s), z);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+              if (r < rows) acc[r] = add_rn(acc[r], mul_rn(xv[r][q], u));
+          } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+              if (r < rows) acc[r] = add_rn(acc[r], mul_rn(mul_rn(xv[r][q], wf[j]), s));
+          }
+        }
+      }
+    }
+  };
+  using Full = std::integral_constant<bool, true>;
+  using Part = std::integral_constant<bool, false>;
+  auto issue_any = [&](Batch& bt, int k0, int kend) __attribute__((always_inline)) {
+    if (k0 + U <= kend)
+      issue(bt, k0, kend, Full{});
+    else
+      issue(bt, k0, kend, Part{});
+  };
+  auto compute_any = [&](const Batch& bt, int k0, int kend, int kc) __attribute__((always_inline)) {
+    if (k0 + U <= kend)
+      compute(bt, k0, kend, kc, Full{});
+    else
+      compute(bt, k0, kend, kc, Part{});
+  };
+
+  const int Ki = (int)K;  // K < 2^31 (validated)
+  for (int kc = 0; kc < Ki; kc += kExactKC) {
+    const int kend = min(Ki, kc + kExactKC);
+    const int kn = kend - kc;
+    __syncthreads();  // the previous chunk's x has been used (and the NF4 table written)
+    for (int i = threadIdx.x; i < R * kExactKC; i += kExactThreads) {
+      const int r = i / kExactKC, j = i - r * kExactKC;
+      xs[r][j] = r < rows && j < kn ? load_f(d.x, (m0 + r) * K + kc + j, d.x_dt) : 0.0f;
+    }
+    __syncthreads();
+    // Two batches of requests in flight: batch b + 1 is requested before batch b is computed.
+    start(kc);
+    Batch A, Bt;
+    issue_any(A, kc, kend);
+    for (int k0 = kc; k0 < kend; k0 += 2 * U) {
+      const bool more = k0 + U < kend;
+      if (more) issue_any(Bt, k0 + U, kend);
+      compute_any(A, k0, kend, kc);
+      if (k0 + 2 * U < kend) issue_any(A, k0 + 2 * U, kend);
+      if (more) compute_any(Bt, k0 + U, kend, kc);
     }
   }
+  if (!active) return;
 #pragma unroll
-  for (int r = 0; r < kExactRows; ++r)
+  for (int r = 0; r < R; ++r)
     if (r < rows) store_f(d.out, (m0 + r) * N + n, d.x_dt, act_ref(acc[r], d.act));
+}
+
+// Rows per thread of the reference-order kernel: 8 when the grid has two waves per SIMD of a
+// 256-CU part even so, else 1.
+static int exact_rows(const QDenseDesc& d) {
+  const int64_t col_blocks = (d.N + kExactThreads - 1) / kExactThreads;
+  return d.M * col_blocks * (kExactThreads / 64) > 2048 ? 8 : 1;
 }
 
 // =============================================================================================
@@ -369,10 +552,25 @@ int qdense_run(mx_backend* b, const QDenseDesc& d) {
     case QPath::kDequant:
       return qdense_dequant_run(b, d, name);
     default: {
-      dim3 grid((unsigned)((d.N + kExactThreads - 1) / kExactThreads),
-                (unsigned)((d.M + kExactRows - 1) / kExactRows));
+      const int R = exact_rows(d);
+      dim3 grid((unsigned)((d.N + kExactThreads - 1) / kExactThreads), (unsigned)((d.M + R - 1) / R));
       if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "FusedQuantizedDense: M too large for the exact path");
-      return launch(b, name, [&] { dispatch(qdense_exact_kernel, grid, kExactThreads, 0, st, d); });
+      // The scale varies along K unless there is one per column (block_axis 0, one group).
+      const bool sk = d.block_axis == 1 || d.block_size < d.K;
+      return launch(b, name, [&] {
+        auto go = [&](auto kern) { dispatch(kern, grid, kExactThreads, 0, st, d); };
+        if (R == 8) {
+          if (d.zp)
+            sk ? go(qdense_exact_kernel<8, true, true>) : go(qdense_exact_kernel<8, true, false>);
+          else
+            sk ? go(qdense_exact_kernel<8, false, true>) : go(qdense_exact_kernel<8, false, false>);
+        } else {
+          if (d.zp)
+            sk ? go(qdense_exact_kernel<1, true, true>) : go(qdense_exact_kernel<1, true, false>);
+          else
+            sk ? go(qdense_exact_kernel<1, false, true>) : go(qdense_exact_kernel<1, false, false>);
+        }
+      });
     }
   }
 }
