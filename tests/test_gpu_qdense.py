@@ -67,6 +67,40 @@ def test_exact_bf16_ragged_shapes(backend, shape):
     assert np.array_equal(r.run(), O.expected_output(p))
 
 
+# The reference-order kernel's own paths, forced with the exact option: rows longer than one LDS
+# chunk of x (512 values, the last batch partial), odd N with 4-bit storage (the nibble of
+# element k*N + n alternates with k), bf16 scales / zero points stepped along K (their position
+# in the 32-bit word alternates too), and the 8-rows-per-thread variant taken by grids with many
+# rows.
+EXACT_CASES = [
+    # M, K, N, w_dtype, x_dtype, scale_dtype, block_axis, block_size, zp, scheme
+    (3, 1100, 67, O.DT_INT4, O.DT_FLOAT32, O.DT_FLOAT32, 0, None, False, O.QUANT_LINEAR),   # one scale per column
+    (3, 1100, 67, O.DT_INT4, O.DT_FLOAT32, O.DT_BFLOAT16, 0, 48, False, O.QUANT_LINEAR),    # groups across batches
+    (2, 700, 45, O.DT_UINT4, O.DT_FLOAT32, O.DT_BFLOAT16, 1, 16, True, O.QUANT_LINEAR),     # reference layout, zp
+    (2, 530, 31, O.DT_UINT4, O.DT_BFLOAT16, O.DT_FLOAT32, 1, 7, False, O.QUANT_NF4),        # NF4, odd N
+    (600, 40, 256, O.DT_INT8, O.DT_FLOAT32, O.DT_FLOAT32, 0, None, False, O.QUANT_LINEAR),  # 8 rows per thread
+    (600, 40, 130, O.DT_INT4, O.DT_FLOAT32, O.DT_BFLOAT16, 0, 16, True, O.QUANT_LINEAR),    # 8 rows, zp, groups
+]
+
+
+@pytest.mark.parametrize("case", EXACT_CASES, ids=lambda c: f"M{c[0]}K{c[1]}N{c[2]}_w{c[3]}_ax{c[6]}_B{c[7]}_zp{int(c[8])}_s{c[9]}")
+def test_exact_kernel_paths(case):
+    import compute_amd as ca
+    M, K, N, w_dtype, x_dtype, s_dtype, axis, B, zp, scheme = case
+    p = O.make_problem(M, K, N, w_dtype=w_dtype, x_dtype=x_dtype, scale_dtype=s_dtype, block_axis=axis,
+                       block_size=B, bias=True, zp=zp, scheme=scheme, act=O.ACT_SILU, seed=M + K + N)
+    ex = ca.New("exact")
+    try:
+        r = QDenseRun(ex, p)
+        assert r.plan() == "qdense_exact"
+        y = r.run()
+    finally:
+        ex.Finalize()
+    want = O.expected_output(p)
+    assert np.array_equal(y.view(np.uint16 if x_dtype == O.DT_BFLOAT16 else np.uint32),
+                          want.view(np.uint16 if x_dtype == O.DT_BFLOAT16 else np.uint32))
+
+
 def test_empty_and_zero_k(backend):
     p = O.make_problem(0, 16, 8, w_dtype=O.DT_INT8, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32,
                        block_axis=1, block_size=8)
