@@ -21,6 +21,12 @@
 //                      f32 accumulation bound.
 //   ggml_embed       — one thread per output value (the reference's arithmetic, bit-identical);
 //                      indices of any integer dtype, bad indices reported after the launch.
+// Plans: up to 4 rows the GEMV; problems of at most 2^24 multiply-adds the exact kernel; up to 12
+// rows the GEMV once per group of four rows; past that the rows dequantised once to f32 [N, K]
+// (each value exactly as the reference forms it), contracted on the f32 matrix cores (DotGeneral
+// with a transposed right-hand side) and the bias and activation applied in place, within the f32
+// accumulation bound of the reference's sum.  The exact backend option selects the exact kernel;
+// the allocation-free entry point never takes the dequantised path.
 #include <algorithm>
 #include <cstring>
 
@@ -361,11 +367,6 @@ static size_t ggml_gemv_lds(const GgmlDesc& d, int* ch) {
   return bytes;
 }
 
-bool ggml_gemv_fits(const GgmlDesc& d) {
-  int ch;
-  return ggml_gemv_lds(d, &ch) != 0;
-}
-
 template <int T, int CH>
 static void launch_gemv_ch(const GgmlDesc& d, int grid, size_t lds, hipStream_t st) {
   switch (d.M) {
@@ -386,32 +387,190 @@ static void launch_gemv_t(const GgmlDesc& d, int grid, size_t lds, int ch, hipSt
     launch_gemv_ch<T, 8>(d, grid, lds, st);
 }
 
-const char* ggml_plan_name(const GgmlDesc& d) {
-  if (d.M == 0 || d.N == 0) return "empty";
-  return ggml_gemv_fits(d) ? "ggml_gemv" : "ggml_dense_exact";
+
+// Prefill: the rows dequantised to f32 [N, K], each value as the reference forms it (the
+// arithmetic of ggml_value, the type fixed at compile time).  A workgroup per row at a
+// time: the row's bytes staged in LDS with coalesced 2-byte loads (every block size is even),
+// then eight consecutive values (one block's) per thread decoded from LDS and written as two
+// 16-byte stores.  Rows of up to kDqRowBytes bytes (dynamic LDS of the row's size).
+constexpr int kDqRowBytes = 64 * 1024;
+
+// Values i .. i+7 of a block (i a multiple of 8), as ggml_value forms each one, with what the
+// eight share (the block scale, a K-quant sub-block's scale and minimum) formed once.
+template <int T>
+__device__ __forceinline__ void ggml_values8(const uint8_t* blk, int i, float* v) {
+  if constexpr (T == MX_GGML_Q8_0) {
+    const float d = f16_at(blk);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = mul_rn(d, (float)(int8_t)blk[2 + i + e]);
+  } else if constexpr (T == MX_GGML_Q4_0 || T == MX_GGML_IQ4_NL) {
+    const float d = f16_at(blk);
+    const uint8_t* q = blk + 2 + (i & 15);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t nib = i < 16 ? q[e] & 15u : (uint32_t)q[e] >> 4;
+      v[e] = T == MX_GGML_Q4_0 ? mul_rn(d, (float)((int)nib - 8)) : mul_rn(d, kIQ4NL[nib]);
+    }
+  } else if constexpr (T == MX_GGML_Q4_K) {
+    const int chunk = i >> 6, w = i & 63, j = 2 * chunk + (w >> 5);
+    uint32_t sc, m;
+    scale_min_k4(j, blk + 4, &sc, &m);
+    const float d1 = mul_rn(f16_at(blk), (float)sc), min1 = mul_rn(f16_at(blk + 2), (float)m);
+    const uint8_t* q = blk + 16 + 32 * chunk + (w & 31);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = add_rn(mul_rn(d1, (float)(w < 32 ? q[e] & 15u : (uint32_t)q[e] >> 4)), -min1);
+  } else {  // MX_GGML_Q6_K
+    const int h = i >> 7, r = i & 127, j = r >> 5, l = r & 31;
+    const float ds = mul_rn(f16_at(blk + 208), (float)(int)(int8_t)blk[192 + 8 * h + 2 * j + (l >> 4)]);
+    const uint8_t* ql = blk + 64 * h + 32 * (j & 1) + l;
+    const uint8_t* qh = blk + 128 + 32 * h + l;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t nib = (j >> 1) ? (uint32_t)ql[e] >> 4 : ql[e] & 15u;
+      const uint32_t hi2 = ((uint32_t)qh[e] >> (2 * j)) & 3u;
+      v[e] = mul_rn(ds, (float)((int)(nib | (hi2 << 4)) - 32));
+    }
+  }
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void ggml_dequant_f32_kernel(GgmlDesc d, float* __restrict__ wt) {
+  constexpr int vpb = T == MX_GGML_Q4_K || T == MX_GGML_Q6_K ? 256 : 32;
+  constexpr int vsh = vpb == 256 ? 8 : 5;
+  extern __shared__ __align__(16) uint16_t rs[];
+  const uint8_t* rb = reinterpret_cast<const uint8_t*>(rs);
+  const int bpb = ggml_bpb(T);
+  const int K8 = (int)(d.K / 8), H = (int)(d.bpr / 2);
+  for (int64_t n = blockIdx.x; n < d.N; n += gridDim.x) {
+    const uint16_t* row = reinterpret_cast<const uint16_t*>(d.w + n * d.bpr);
+    for (int h = threadIdx.x; h < H; h += blockDim.x) rs[h] = row[h];
+    __syncthreads();
+    float4* out = reinterpret_cast<float4*>(wt + n * d.K);
+    for (int j = threadIdx.x; j < K8; j += blockDim.x) {
+      const int k = 8 * j;
+      const uint8_t* blk = rb + (k >> vsh) * bpb;
+      const int i = k & (vpb - 1);
+      float v[8];
+      ggml_values8<T>(blk, i, v);
+      out[2 * j] = make_float4(v[0], v[1], v[2], v[3]);
+      out[2 * j + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    __syncthreads();
+  }
+}
+
+// In place on the f32 sums: the bias added after the sum (the reference's order), then the
+// reference activation.
+__global__ void ggml_epilogue_kernel(float* __restrict__ y, const float* __restrict__ bias, int act, int64_t M,
+                                     int64_t N) {
+  const int64_t total = M * N;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    float v = y[i];
+    if (bias) v = add_rn(v, bias[i % N]);
+    y[i] = act_ref(v, act);
+  }
+}
+
+enum class GPlan { kEmpty, kGemv, kDequant, kExact };
+
+static GPlan ggml_plan(const mx_backend* b, const GgmlDesc& d) {
+  if (d.M == 0 || d.N == 0) return GPlan::kEmpty;
+  if (b->exact_qdense) return GPlan::kExact;
+  int ch;
+  if (d.M <= 4 && ggml_gemv_lds(d, &ch)) return GPlan::kGemv;
+  // Problems this small keep the reference's order (bit-identical).
+  if (d.M * d.K * d.N <= ((int64_t)1 << 24)) return GPlan::kExact;
+  GgmlDesc g4 = d;
+  g4.M = 4;
+  const bool gemv4 = ggml_gemv_lds(g4, &ch) != 0;
+  // The weights read once per group of four rows (about 40 us a group at [4096] x 11008 rows),
+  // until one dequantisation and a matrix-core contraction (about 145 us there at 32 rows)
+  // cost less; both scale with the weight bytes, so the crossover holds across shapes.
+  if (d.M <= 12 && gemv4) return GPlan::kGemv;
+  // The dequantised matrix is a device allocation: not for the allocation-free entry point.
+  if (!b->noalloc_active && d.N * d.K * 4 <= ((int64_t)8 << 30) && d.bpr <= kDqRowBytes && d.bpr % 2 == 0 && (uintptr_t)d.w % 2 == 0 &&
+      (uintptr_t)d.x % 16 == 0)
+    return GPlan::kDequant;
+  return gemv4 ? GPlan::kGemv : GPlan::kExact;
+}
+
+const char* ggml_plan_name(const mx_backend* b, const GgmlDesc& d) {
+  switch (ggml_plan(b, d)) {
+    case GPlan::kEmpty: return "empty";
+    case GPlan::kGemv: return "ggml_gemv";
+    case GPlan::kDequant: return "ggml_dequant_f32_mfma";
+    default: return "ggml_dense_exact";
+  }
 }
 
 int ggml_dense_run(mx_backend* b, const GgmlDesc& d) {
   MX_TRY(check_device(b));
-  if (d.M == 0 || d.N == 0) return MX_OK;
   hipStream_t st = b->stream;
-  int ch = 0;
-  const size_t lds = ggml_gemv_lds(d, &ch);
-  if (lds) {
-    const int grid = (int)std::min<int64_t>((d.N + kGvWaves - 1) / kGvWaves, 2 * (int64_t)std::max(b->num_cus, 1));
-    return launch(b, "ggml_gemv", [&] {
-      switch (d.type) {
-        case MX_GGML_Q4_0: launch_gemv_t<MX_GGML_Q4_0>(d, grid, lds, ch, st); break;
-        case MX_GGML_Q8_0: launch_gemv_t<MX_GGML_Q8_0>(d, grid, lds, ch, st); break;
-        case MX_GGML_IQ4_NL: launch_gemv_t<MX_GGML_IQ4_NL>(d, grid, lds, ch, st); break;
-        case MX_GGML_Q4_K: launch_gemv_t<MX_GGML_Q4_K>(d, grid, lds, ch, st); break;
-        default: launch_gemv_t<MX_GGML_Q6_K>(d, grid, lds, ch, st); break;
+  switch (ggml_plan(b, d)) {
+    case GPlan::kEmpty:
+      return MX_OK;
+    case GPlan::kGemv: {
+      // Groups of up to four rows, one launch each.
+      for (int64_t m0 = 0; m0 < d.M; m0 += 4) {
+        GgmlDesc g = d;
+        g.x = d.x + m0 * d.K;
+        g.out = d.out + m0 * d.N;
+        g.M = std::min<int64_t>(4, d.M - m0);
+        int ch = 0;
+        const size_t lds = ggml_gemv_lds(g, &ch);
+        if (!lds) return set_error(MX_ERR_INVALID, "internal: GGML GEMV plan without a launch");
+        const int grid = (int)std::min<int64_t>((g.N + kGvWaves - 1) / kGvWaves, 2 * (int64_t)std::max(b->num_cus, 1));
+        MX_TRY(launch(b, "ggml_gemv", [&] {
+          switch (g.type) {
+            case MX_GGML_Q4_0: launch_gemv_t<MX_GGML_Q4_0>(g, grid, lds, ch, st); break;
+            case MX_GGML_Q8_0: launch_gemv_t<MX_GGML_Q8_0>(g, grid, lds, ch, st); break;
+            case MX_GGML_IQ4_NL: launch_gemv_t<MX_GGML_IQ4_NL>(g, grid, lds, ch, st); break;
+            case MX_GGML_Q4_K: launch_gemv_t<MX_GGML_Q4_K>(g, grid, lds, ch, st); break;
+            default: launch_gemv_t<MX_GGML_Q6_K>(g, grid, lds, ch, st); break;
+          }
+        }));
       }
-    });
+      return MX_OK;
+    }
+    case GPlan::kDequant: {
+      void* wt = nullptr;
+      MX_TRY(dev_alloc(b, (size_t)(d.N * d.K) * 4, &wt));
+      const int rows = (int)std::min<int64_t>(d.N, 8 * (int64_t)std::max(b->num_cus, 1));
+      const size_t lds = (size_t)(d.bpr + 15) / 16 * 16;
+      int rc = launch(b, "ggml_dequant_f32", [&] {
+        switch (d.type) {
+          case MX_GGML_Q4_0: dispatch(ggml_dequant_f32_kernel<MX_GGML_Q4_0>, rows, 256, lds, st, d, (float*)wt); break;
+          case MX_GGML_Q8_0: dispatch(ggml_dequant_f32_kernel<MX_GGML_Q8_0>, rows, 256, lds, st, d, (float*)wt); break;
+          case MX_GGML_IQ4_NL: dispatch(ggml_dequant_f32_kernel<MX_GGML_IQ4_NL>, rows, 256, lds, st, d, (float*)wt); break;
+          case MX_GGML_Q4_K: dispatch(ggml_dequant_f32_kernel<MX_GGML_Q4_K>, rows, 256, lds, st, d, (float*)wt); break;
+          default: dispatch(ggml_dequant_f32_kernel<MX_GGML_Q6_K>, rows, 256, lds, st, d, (float*)wt); break;
+        }
+      });
+      if (rc == MX_OK) {
+        DotDesc dd{};
+        dd.lhs = d.x;
+        dd.rhs = wt;
+        dd.out = d.out;
+        dd.B = 1;
+        dd.M = d.M;
+        dd.K = d.K;
+        dd.N = d.N;
+        dd.rhs_transposed = true;
+        dd.in_dt = MX_DTYPE_FLOAT32;
+        dd.out_dt = MX_DTYPE_FLOAT32;
+        rc = dot_run(b, dd);
+      }
+      if (rc == MX_OK)
+        rc = launch(b, "ggml_epilogue", [&] { dispatch(ggml_epilogue_kernel, 1024, 256, 0, st, d.out, d.bias, d.act, d.M, d.N); });
+      dev_free(b, wt);  // stream-ordered pool: later users run after these kernels
+      return rc;
+    }
+    default: {
+      dim3 grid((unsigned)((d.N + kGxThreads - 1) / kGxThreads), (unsigned)((d.M + kGxRows - 1) / kGxRows));
+      if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "FusedQuantizedDense(GGML): M too large");
+      return launch(b, "ggml_dense_exact", [&] { dispatch(ggml_dense_exact_kernel, grid, kGxThreads, 0, st, d); });
+    }
   }
-  dim3 grid((unsigned)((d.N + kGxThreads - 1) / kGxThreads), (unsigned)((d.M + kGxRows - 1) / kGxRows));
-  if (grid.y > 65535u) return set_error(MX_ERR_INVALID, "FusedQuantizedDense(GGML): M too large");
-  return launch(b, "ggml_dense_exact", [&] { dispatch(ggml_dense_exact_kernel, grid, kGxThreads, 0, st, d); });
 }
 
 // =============================================================================================

@@ -264,8 +264,8 @@ struct GgmlEmbedDesc {
   int idx_dt = 0, type = 0;
 };
 int ggml_block_geometry(int type, int* vpb, int* bpb);
-bool ggml_gemv_fits(const GgmlDesc& d);
-const char* ggml_plan_name(const GgmlDesc& d);
+// Plan and launch; the backend's exact option selects the reference-order kernel at every size.
+const char* ggml_plan_name(const mx_backend* b, const GgmlDesc& d);
 int ggml_dense_run(mx_backend* b, const GgmlDesc& d);
 int ggml_embed_run(mx_backend* b, const GgmlEmbedDesc& e);
 

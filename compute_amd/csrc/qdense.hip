@@ -481,9 +481,8 @@ static const char* path_name(const QDenseDesc& d, QPath p) {
 }
 
 int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name) {
-  (void)b;
   if (d.scheme == MX_QUANT_GGML) {
-    *name = ggml_plan_name(ggml_desc(d));
+    *name = ggml_plan_name(b, ggml_desc(d));
     return MX_OK;
   }
   const QPath p = choose_path(b, d);

@@ -377,7 +377,8 @@ int mx_qdense_plan(mx_backend* b, const mx_qdense_args* args, char* buf, size_t 
  * ends; a problem whose split-K needs more returns MX_ERR_INVALID before anything is launched.
  * Results are bit-identical to mx_qdense's, except where mx_qdense would dequantise the weights
  * into an f32 copy (reference layout at prefill size): that problem runs the exact kernel, whose
- * result is bit-identical to the reference's. Every call on one GPU shares the array, from any
+ * result is bit-identical to the reference's; GGML rows there run the decode GEMV once per group
+ * of four rows (within the f32 accumulation bound of the reference's sum). Every call on one GPU shares the array, from any
  * backend: calls that overlap on one GPU (several streams or backends) race. Launches are not
  * recorded in the backend's kernel profile. */
 #define MX_QDENSE_NOALLOC_SCRATCH_BYTES (16u << 20)

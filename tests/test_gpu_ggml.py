@@ -1,15 +1,20 @@
 """GPU parity of the GGML block formats (compute_amd/csrc/ggml.hip) against the CPU oracle.
 
-- ggml_dense_exact (M > 4 rows, or anything the GEMV does not take): bit-identical f32 output,
-  bias and activation included (the reference's order: dot, then bias, then activation).
-- ggml_gemv (M <= 4): f32 accumulation bar — |y - exact| <= 1e-5 * sum|x*w| per output (the
-  kernel sums in another order), identical bits on repeated calls, rows whose byte length is
-  not a multiple of 16 (staging skew), the decode shape [1, 4096] x 11008 rows.
+- ggml_dense_exact (problems of at most 2^24 multiply-adds past 4 rows, anything the GEMV does
+  not take, and every size under the exact backend option): bit-identical f32 output, bias and
+  activation included (the reference's order: dot, then bias, then activation).
+- ggml_gemv (M <= 4, and M <= 12 as one launch per group of four rows): f32 accumulation bar —
+  |y - exact| <= 1e-5 * sum|x*w| per output (the kernel sums in another order), identical bits
+  on repeated calls, rows whose byte length is not a multiple of 16 (staging skew), the decode
+  shape [1, 4096] x 11008 rows, ragged last groups (M = 5, 11).
+- ggml_dequant_f32_mfma (M > 12): rows dequantised to f32, contracted on the matrix cores, bias
+  and activation after the sum; the same accumulation bar, activation within float tolerance.
 - QuantizedEmbeddingLookup: bit-identical rows for every index dtype; an index outside
   [0, vocab) fails the Execute call, as the reference's executor does.
 """
 import numpy as np
 import pytest
+from scipy.special import erf, expit
 
 import compute_amd as ca
 from compute_amd import _lib
@@ -102,6 +107,81 @@ def test_gemv_rows_not_16_byte_aligned(backend, t, K):
     r = GgmlRun(backend, t, x, w, b)
     assert r.plan() == "ggml_gemv"
     accumulation_check(r.run(), x, w, t, b)
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("M,N", [(5, 3400), (8, 2100), (11, 1500)])
+def test_gemv_row_groups_accumulation_bound(backend, t, M, N):
+    # Past 2^24 multiply-adds and up to 12 rows: the GEMV once per group of four rows.
+    assert M * 1024 * N > 1 << 24
+    x, w, b = problem(t, M, 1024, N)
+    r = GgmlRun(backend, t, x, w, b)
+    assert r.plan() == "ggml_gemv"
+    got = r.run()
+    accumulation_check(got, x, w, t, b)
+    assert np.array_equal(got.view(np.uint32), r.run().view(np.uint32))
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("M", [13, 65, 200])
+def test_dequant_mfma_accumulation_bound(backend, t, M):
+    N = 264 if M > 64 else 1300
+    assert M * 1024 * N > 1 << 24
+    x, w, b = problem(t, M, 1024, N)
+    r = GgmlRun(backend, t, x, w, b)
+    assert r.plan() == "ggml_dequant_f32_mfma"
+    got = r.run()
+    accumulation_check(got, x, w, t, b)
+    assert np.array_equal(got.view(np.uint32), r.run().view(np.uint32))
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_mfma_values_exact(backend, t):
+    # x = identity: every sum has one nonzero term, so the output is the dequantised matrix
+    # transposed, each value as the reference forms it (compared with ==, so +0 equals -0).
+    K, N = 512, 128
+    w = O.ggml_random_rows(int(t), N, K, RNG)
+    x = np.eye(K, dtype=np.float32)
+    r = GgmlRun(backend, t, x, w)
+    assert r.plan() == "ggml_dequant_f32_mfma"
+    deq = O.ggml_embedding(w, int(t), np.arange(N))
+    assert (r.run() == deq.T).all()
+
+
+@pytest.mark.parametrize("t", [ca.GGMLQ4_0, ca.GGMLQ6_K])
+@pytest.mark.parametrize("act", [ca.ActivationGelu, ca.ActivationSilu])
+def test_dequant_mfma_activation(backend, t, act):
+    x, w, b = problem(t, 96, 512, 400)
+    r = GgmlRun(backend, t, x, w, b, act)
+    assert r.plan() == "ggml_dequant_f32_mfma"
+    # The accumulation bar carried through the activation: GELU's and SiLU's slopes stay below
+    # 1.2, and the activation's own f32 rounding adds a few ulps of the result.
+    exact, ab = O.ggml_dense_f64(x, w, int(t), b)
+    if act == ca.ActivationGelu:
+        want = 0.5 * exact * (1.0 + erf(exact / np.sqrt(2.0)))
+    else:
+        want = exact * expit(exact)
+    err = np.abs(r.run().astype(np.float64) - want)
+    bound = 1.2 * 1e-5 * ab + 4 * np.finfo(np.float32).eps * np.abs(want) + 1e-30
+    assert (err <= bound).all(), f"worst {np.max(err / bound)} x the bound"
+
+
+@pytest.mark.parametrize("t", [ca.GGMLQ4_0, ca.GGMLQ4_K])
+@pytest.mark.parametrize("M", [8, 96])
+def test_exact_option_keeps_reference_order(t, M):
+    # The exact backend option selects the reference-order kernel at sizes that otherwise take
+    # the GEMV row groups or the dequantised matrix-core path.
+    x, w, b = problem(t, M, 1024, 2100 if M < 16 else 300)
+    assert M * 1024 * (2100 if M < 16 else 300) > 1 << 24
+    ex = ca.New("exact")
+    try:
+        r = GgmlRun(ex, t, x, w, b, ca.ActivationSilu)
+        assert r.plan() == "ggml_dense_exact"
+        got = r.run()
+    finally:
+        ex.Finalize()
+    want = O.ggml_dense(x, w, int(t), b, int(ca.ActivationSilu))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("t", [ca.GGMLQ4_0, ca.GGMLQ4_K])

@@ -6,7 +6,9 @@ static per-GPU array, so on the skinny, GEMV and GEMM paths its result must be b
 mx_qdense's, and within the oracle bars of those paths (bf16 outputs rel 1e-2 / abs 1e-3 of the
 reference's f32 result).  Where mx_qdense dequantises the weights into an f32 copy, the
 allocation-free call runs the exact kernel: its result must equal the oracle's restatement of the
-reference loop bit for bit, and mx_qdense's within the f32 accumulation bound.  Each case makes two
+reference loop bit for bit, and mx_qdense's within the f32 accumulation bound.  GGML rows past 12
+rows, which mx_qdense also dequantises, take the GEMV once per group of four rows on the
+allocation-free call, within the same bound.  Each case makes two
 calls in a row, the second on a smaller problem, as a caller reusing the shared array would.
 """
 import ctypes as C
@@ -145,3 +147,37 @@ def test_noalloc_second_backend_shares_array():
         assert_bf16_close(got, O.qdense_f32(SKINNY[0], threads=8), what="second backend")
     finally:
         b2.Finalize()
+
+
+def test_noalloc_ggml_prefill_takes_gemv_groups(backend):
+    """GGML rows past 12 rows: mx_qdense dequantises them into an f32 copy for the matrix cores;
+    the allocation-free call runs the GEMV once per group of four rows instead, within the same
+    f32 accumulation bound.  The second, smaller call (8 rows) takes the GEMV groups on both."""
+    rng = np.random.default_rng(11)
+    t = int(ca.GGMLQ4_K)
+    for M, K, N, plan in ((32, 1024, 1536, "ggml_dequant_f32_mfma"), (8, 1024, 2400, "ggml_gemv")):
+        w = O.ggml_random_rows(t, N, K, rng)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        bias = rng.standard_normal(N).astype(np.float32)
+        up = lambda a, sh: backend.BufferFromFlatData(0, np.ascontiguousarray(a).ravel(), sh)
+        bx, bw, bb = up(x, ca.Shape(ca.Float32, M, K)), up(w, ca.Shape(ca.Uint8, N, w.shape[1])), up(bias, ca.Shape(ca.Float32, N))
+        outs = [up(np.zeros(M * N, np.float32), ca.Shape(ca.Float32, M, N)) for _ in range(2)]
+
+        def args(out):
+            a = _lib.mx_qdense_args()
+            a.x, a.w, a.out = bx.DevicePtr(), bw.DevicePtr(), out.DevicePtr()
+            a.bias, a.bias_dtype = bb.DevicePtr(), O.DT_FLOAT32
+            a.M, a.K, a.N = M, K, N
+            a.x_dtype, a.scheme, a.ggml_type = O.DT_FLOAT32, int(ca.QuantGGML), t
+            return a
+
+        assert backend.QDensePlan(args(outs[0])) == plan
+        for entry, out in zip(("mx_qdense", "mx_qdense_noalloc"), outs):
+            rc = getattr(backend._lib, entry)(backend._h, C.byref(args(out)))
+            assert rc == _lib.MX_OK, f"{entry}: {backend._lib.mx_last_error().decode()}"
+        ref, got = (o.ToFlatData().reshape(M, N) for o in outs)
+        exact, ab = O.ggml_dense_f64(x, w, t, bias)
+        for y in (ref, got):
+            assert (np.abs(y.astype(np.float64) - exact) <= 1e-5 * ab + 1e-30).all()
+        if plan == "ggml_gemv":
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
