@@ -21,7 +21,7 @@
 //                      f32 accumulation bound.
 //   ggml_embed       — one thread per output value (the reference's arithmetic, bit-identical);
 //                      indices of any integer dtype, bad indices reported after the launch.
-// Plans: up to 4 rows the GEMV; problems of at most 2^24 multiply-adds the exact kernel; up to 12
+// Plans: up to 4 rows the GEMV; problems of at most 2^24 multiply-adds the exact kernel; up to 20
 // rows the GEMV once per group of four rows; past that the rows dequantised once to f32 [N, K]
 // (each value exactly as the reference forms it), contracted on the f32 matrix cores (DotGeneral
 // with a transposed right-hand side) and the bias and activation applied in place, within the f32
@@ -163,9 +163,11 @@ __global__ __launch_bounds__(kGxThreads) void ggml_dense_exact_kernel(GgmlDesc d
 // =============================================================================================
 // Decode GEMV.
 // =============================================================================================
-constexpr int kGvWaves = 8;
-constexpr int kGvThreads = 64 * kGvWaves;
+// Waves per workgroup: 16 (one workgroup per CU, x staged once per CU) where the kernel stays
+// within 128 registers (M = 1, and M = 2 with rows of up to 4 chunks per lane), else 8.
+constexpr int kGvWavesMax = 16;
 constexpr int kGvPad = 36;  // floats per 32-value unit of x in LDS
+constexpr int kGvXB = 4;    // 16-byte x loads per thread in flight while staging
 
 // Four bytes of LDS at a 2-byte-aligned address.
 __device__ __forceinline__ uint32_t lds_dword2(const uint8_t* p) {
@@ -268,8 +270,9 @@ __device__ __forceinline__ void ggml_unit(const uint8_t* row, int u, const float
 }
 
 // CH: 16-byte chunks of a row per lane (the row, with its alignment skew, is at most 64*CH chunks).
-template <int T, int MR, int CH>
-__global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d) {
+template <int T, int MR, int CH, int WV>
+__global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
+  constexpr int kGvWaves = WV, kGvThreads = 64 * WV;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int kRowBytes = 64 * CH * 16;
   const int K = (int)d.K, units = K >> 5;
@@ -286,35 +289,65 @@ __global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d) {
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(d.w), (short)0, (int)total, 0x00020000);
   // A row is loaded into registers one row ahead (16-byte loads from the aligned address at or
   // below its start; the row then begins `skew` bytes into the staging buffer), so its loads
-  // travel while the previous row is computed.
+  // travel while the previous row is computed.  Chunks past the row's end are given an offset
+  // past the buffer's range: they read 0 without a memory access.  (Two rows ahead took 16 more
+  // registers, past the 128 that keep two workgroups on a CU, and measured slower.)
   u32x4_v pre[CH];
-  auto issue = [&](int64_t row) {
-    const uint32_t a0 = (uint32_t)((min(row, d.N - 1) * d.bpr) & ~(int64_t)15);
+  auto issue = [&](int64_t row, u32x4_v (&dst)[CH]) {
+    const int64_t r = min(row, d.N - 1);
+    const uint32_t a0 = (uint32_t)((r * d.bpr) & ~(int64_t)15), end = (uint32_t)(r * d.bpr + d.bpr);
 #pragma unroll
-    for (int i = 0; i < CH; ++i) pre[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, a0 + 16u * (lane + 64 * i), 0, 0);
+    for (int i = 0; i < CH; ++i) {
+      const uint32_t off = a0 + 16u * (lane + 64 * i);
+      dst[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off < end ? off : 0x7FFFFFF0u, 0, 0);
+    }
   };
   const int64_t stride = (int64_t)gridDim.x * kGvWaves;
   int64_t n = (int64_t)blockIdx.x * kGvWaves + wave;
-  if (n < d.N) issue(n);  // before staging x: the first row travels meanwhile
-  for (int i = t; i < MR * K; i += kGvThreads) {
-    const int m = i / K, k = i - m * K;
-    xs[(m * units + (k >> 5)) * kGvPad + (k & 31)] = d.x[(size_t)m * K + k];
+  if (n < d.N) issue(n, pre);  // before staging x: the first row travels meanwhile
+  // x staged as [MR][units][kGvPad] floats with 16-byte loads, kGvXB of them issued before their
+  // stores (K % 32 == 0, x 16-byte aligned).
+  {
+    const int q4 = MR * K / 4;
+    for (int base = t; base < q4; base += kGvXB * kGvThreads) {
+      float4 v[kGvXB];
+#pragma unroll
+      for (int j = 0; j < kGvXB; ++j) {
+        const int i = base + j * kGvThreads;
+        if (i < q4) v[j] = reinterpret_cast<const float4*>(d.x)[i];
+      }
+#pragma unroll
+      for (int j = 0; j < kGvXB; ++j) {
+        const int i = base + j * kGvThreads;
+        if (i < q4) {
+          const int m = 4 * i / K, k = 4 * i - m * K;
+          *reinterpret_cast<float4*>(xs + (m * units + (k >> 5)) * kGvPad + (k & 31)) = v[j];
+        }
+      }
+    }
   }
   __syncthreads();
-  // Each unit's sum of x, kept in the unit's padding (slot 32), in a fixed order.
+  // Each unit's sum of x, kept in the unit's padding (slot 32), in a fixed order (four partial
+  // sums over the unit's 16-byte chunks, then added in order).
   for (int i = t; i < MR * units; i += kGvThreads) {
     float* xu = xs + (size_t)i * kGvPad;
-    float a = 0.0f;
+    float4 a = reinterpret_cast<const float4*>(xu)[0];
 #pragma unroll
-    for (int l = 0; l < 32; ++l) a += xu[l];
-    xu[32] = a;
+    for (int c = 1; c < 8; ++c) {
+      const float4 v = reinterpret_cast<const float4*>(xu)[c];
+      a.x += v.x;
+      a.y += v.y;
+      a.z += v.z;
+      a.w += v.w;
+    }
+    xu[32] = (a.x + a.y) + (a.z + a.w);
   }
   __syncthreads();
 
   for (; n < d.N; n += stride) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) *(u32x4_v*)(rb + 16 * (lane + 64 * i)) = pre[i];
-    if (n + stride < d.N) issue(n + stride);
+    if (n + stride < d.N) issue(n + stride, pre);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
@@ -352,39 +385,51 @@ __global__ __launch_bounds__(kGvThreads) void ggml_gemv_kernel(GgmlDesc d) {
   }
 }
 
-// Chunks per lane (2, 4 or 8) and LDS of the GEMV for these sizes, or 0 if it does not apply.
-static size_t ggml_gemv_lds(const GgmlDesc& d, int* ch) {
+// Chunks per lane (2, 4 or 8), waves per workgroup (8 or 16) and LDS of the GEMV for these
+// sizes, or 0 if it does not apply.
+static size_t ggml_gemv_lds(const GgmlDesc& d, int* ch, int* waves) {
   if (d.M < 1 || d.M > 4 || d.K % 32 != 0 || d.K > (1 << 20) || d.N * d.bpr + 16 >= ((int64_t)1 << 31) ||
-      (uintptr_t)d.w % 16 != 0)
+      (uintptr_t)d.w % 16 != 0 || (uintptr_t)d.x % 16 != 0)
     return 0;
   const int64_t chunks = (d.bpr + 15 + 15) / 16;  // worst-case skew included
   int c = 2;
   while (c < 8 && 64 * c < chunks) c *= 2;
   if (64 * c < chunks) return 0;
-  const size_t bytes = (size_t)d.M * (d.K / 32) * kGvPad * sizeof(float) + (size_t)kGvWaves * 64 * c * 16;
+  const size_t xb = (size_t)d.M * (d.K / 32) * kGvPad * sizeof(float);
+  int wv = d.M == 1 || (d.M == 2 && c <= 4) ? kGvWavesMax : 8;
+  if (xb + (size_t)wv * 64 * c * 16 > 150 * 1024) wv = 8;
+  const size_t bytes = xb + (size_t)wv * 64 * c * 16;
   if (bytes > 150 * 1024) return 0;
   *ch = c;
+  *waves = wv;
   return bytes;
 }
 
 template <int T, int CH>
-static void launch_gemv_ch(const GgmlDesc& d, int grid, size_t lds, hipStream_t st) {
+static void launch_gemv_ch(const GgmlDesc& d, int grid, size_t lds, int waves, hipStream_t st) {
+  const bool w16 = waves == 16;
   switch (d.M) {
-    case 1: dispatch(ggml_gemv_kernel<T, 1, CH>, grid, kGvThreads, lds, st, d); break;
-    case 2: dispatch(ggml_gemv_kernel<T, 2, CH>, grid, kGvThreads, lds, st, d); break;
-    case 3: dispatch(ggml_gemv_kernel<T, 3, CH>, grid, kGvThreads, lds, st, d); break;
-    default: dispatch(ggml_gemv_kernel<T, 4, CH>, grid, kGvThreads, lds, st, d); break;
+    case 1:
+      w16 ? dispatch(ggml_gemv_kernel<T, 1, CH, 16>, grid, 1024, lds, st, d)
+          : dispatch(ggml_gemv_kernel<T, 1, CH, 8>, grid, 512, lds, st, d);
+      break;
+    case 2:
+      w16 ? dispatch(ggml_gemv_kernel<T, 2, CH, 16>, grid, 1024, lds, st, d)
+          : dispatch(ggml_gemv_kernel<T, 2, CH, 8>, grid, 512, lds, st, d);
+      break;
+    case 3: dispatch(ggml_gemv_kernel<T, 3, CH, 8>, grid, 512, lds, st, d); break;
+    default: dispatch(ggml_gemv_kernel<T, 4, CH, 8>, grid, 512, lds, st, d); break;
   }
 }
 
 template <int T>
-static void launch_gemv_t(const GgmlDesc& d, int grid, size_t lds, int ch, hipStream_t st) {
+static void launch_gemv_t(const GgmlDesc& d, int grid, size_t lds, int ch, int waves, hipStream_t st) {
   if (ch == 2)
-    launch_gemv_ch<T, 2>(d, grid, lds, st);
+    launch_gemv_ch<T, 2>(d, grid, lds, waves, st);
   else if (ch == 4)
-    launch_gemv_ch<T, 4>(d, grid, lds, st);
+    launch_gemv_ch<T, 4>(d, grid, lds, waves, st);
   else
-    launch_gemv_ch<T, 8>(d, grid, lds, st);
+    launch_gemv_ch<T, 8>(d, grid, lds, waves, st);
 }
 
 
@@ -477,16 +522,17 @@ static GPlan ggml_plan(const mx_backend* b, const GgmlDesc& d) {
   if (d.M == 0 || d.N == 0) return GPlan::kEmpty;
   if (b->exact_qdense) return GPlan::kExact;
   int ch;
-  if (d.M <= 4 && ggml_gemv_lds(d, &ch)) return GPlan::kGemv;
+  int wv;
+  if (d.M <= 4 && ggml_gemv_lds(d, &ch, &wv)) return GPlan::kGemv;
   // Problems this small keep the reference's order (bit-identical).
   if (d.M * d.K * d.N <= ((int64_t)1 << 24)) return GPlan::kExact;
   GgmlDesc g4 = d;
   g4.M = 4;
-  const bool gemv4 = ggml_gemv_lds(g4, &ch) != 0;
-  // The weights read once per group of four rows (about 40 us a group at [4096] x 11008 rows),
-  // until one dequantisation and a matrix-core contraction (about 145 us there at 32 rows)
+  const bool gemv4 = ggml_gemv_lds(g4, &ch, &wv) != 0;
+  // The weights read once per group of four rows (about 27 us a group at [4096] x 11008 rows),
+  // until one dequantisation and a matrix-core contraction (about 143 us there past 16 rows)
   // cost less; both scale with the weight bytes, so the crossover holds across shapes.
-  if (d.M <= 12 && gemv4) return GPlan::kGemv;
+  if (d.M <= 20 && gemv4) return GPlan::kGemv;
   // The dequantised matrix is a device allocation: not for the allocation-free entry point.
   if (!b->noalloc_active && d.N * d.K * 4 <= ((int64_t)8 << 30) && d.bpr <= kDqRowBytes && d.bpr % 2 == 0 && (uintptr_t)d.w % 2 == 0 &&
       (uintptr_t)d.x % 16 == 0)
@@ -517,16 +563,20 @@ int ggml_dense_run(mx_backend* b, const GgmlDesc& d) {
         g.out = d.out + m0 * d.N;
         g.M = std::min<int64_t>(4, d.M - m0);
         int ch = 0;
-        const size_t lds = ggml_gemv_lds(g, &ch);
+        int waves = 8;
+        const size_t lds = ggml_gemv_lds(g, &ch, &waves);
         if (!lds) return set_error(MX_ERR_INVALID, "internal: GGML GEMV plan without a launch");
-        const int grid = (int)std::min<int64_t>((g.N + kGvWaves - 1) / kGvWaves, 2 * (int64_t)std::max(b->num_cus, 1));
+        // As many workgroups as are resident at once: 16 waves per CU (four per SIMD at up to 128
+        // registers), fewer where LDS runs out.
+        const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(16 / waves, (int64_t)(160 * 1024) / (int64_t)lds));
+        const int grid = (int)std::min<int64_t>((g.N + waves - 1) / waves, per_cu * std::max(b->num_cus, 1));
         MX_TRY(launch(b, "ggml_gemv", [&] {
           switch (g.type) {
-            case MX_GGML_Q4_0: launch_gemv_t<MX_GGML_Q4_0>(g, grid, lds, ch, st); break;
-            case MX_GGML_Q8_0: launch_gemv_t<MX_GGML_Q8_0>(g, grid, lds, ch, st); break;
-            case MX_GGML_IQ4_NL: launch_gemv_t<MX_GGML_IQ4_NL>(g, grid, lds, ch, st); break;
-            case MX_GGML_Q4_K: launch_gemv_t<MX_GGML_Q4_K>(g, grid, lds, ch, st); break;
-            default: launch_gemv_t<MX_GGML_Q6_K>(g, grid, lds, ch, st); break;
+            case MX_GGML_Q4_0: launch_gemv_t<MX_GGML_Q4_0>(g, grid, lds, ch, waves, st); break;
+            case MX_GGML_Q8_0: launch_gemv_t<MX_GGML_Q8_0>(g, grid, lds, ch, waves, st); break;
+            case MX_GGML_IQ4_NL: launch_gemv_t<MX_GGML_IQ4_NL>(g, grid, lds, ch, waves, st); break;
+            case MX_GGML_Q4_K: launch_gemv_t<MX_GGML_Q4_K>(g, grid, lds, ch, waves, st); break;
+            default: launch_gemv_t<MX_GGML_Q6_K>(g, grid, lds, ch, waves, st); break;
           }
         }));
       }

@@ -6,7 +6,7 @@ static per-GPU array, so on the skinny, GEMV and GEMM paths its result must be b
 mx_qdense's, and within the oracle bars of those paths (bf16 outputs rel 1e-2 / abs 1e-3 of the
 reference's f32 result).  Where mx_qdense dequantises the weights into an f32 copy, the
 allocation-free call runs the exact kernel: its result must equal the oracle's restatement of the
-reference loop bit for bit, and mx_qdense's within the f32 accumulation bound.  GGML rows past 12
+reference loop bit for bit, and mx_qdense's within the f32 accumulation bound.  GGML rows past 20
 rows, which mx_qdense also dequantises, take the GEMV once per group of four rows on the
 allocation-free call, within the same bound.  Each case makes two
 calls in a row, the second on a smaller problem, as a caller reusing the shared array would.
@@ -150,7 +150,7 @@ def test_noalloc_second_backend_shares_array():
 
 
 def test_noalloc_ggml_prefill_takes_gemv_groups(backend):
-    """GGML rows past 12 rows: mx_qdense dequantises them into an f32 copy for the matrix cores;
+    """GGML rows past 20 rows: mx_qdense dequantises them into an f32 copy for the matrix cores;
     the allocation-free call runs the GEMV once per group of four rows instead, within the same
     f32 accumulation bound.  The second, smaller call (8 rows) takes the GEMV groups on both."""
     rng = np.random.default_rng(11)
