@@ -542,6 +542,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const f
   const uint16_t* xr = x + m * D;
   const int t = threadIdx.x;
   const bool cached = D <= (int64_t)kRmsCached * 256;
+  // The row's two constants travel with the x loads (not after the reduction).
+  const float cm = c[m], em = e[m];
   float v[kRmsCached];
   float acc = 0.0f;
   if (cached) {
@@ -564,7 +566,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const f
     if (t < s) sh[t] = add_rn(sh[t], sh[t + s]);
     __syncthreads();
   }
-  const float tt = add_rn(mul_rn(sh[0], c[m]), e[m]);
+  const float tt = add_rn(mul_rn(sh[0], cm), em);
   const float inv = (float)(1.0 / sqrt((double)tt));
   if (cached) {
 #pragma unroll
