@@ -312,10 +312,8 @@ __global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
     for (int base = t; base < q4; base += kGvXB * kGvThreads) {
       float4 v[kGvXB];
 #pragma unroll
-      for (int j = 0; j < kGvXB; ++j) {
-        const int i = base + j * kGvThreads;
-        if (i < q4) v[j] = reinterpret_cast<const float4*>(d.x)[i];
-      }
+      for (int j = 0; j < kGvXB; ++j)  // unconditional (clamped) so that they stay in registers
+        v[j] = reinterpret_cast<const float4*>(d.x)[min(base + j * kGvThreads, q4 - 1)];
 #pragma unroll
       for (int j = 0; j < kGvXB; ++j) {
         const int i = base + j * kGvThreads;
