@@ -135,9 +135,12 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
   }
 }
 
-template <int BK, bool GRP>
+// GPB: blocks per scale group fixed at compile time (1 or 2, folds at fixed steps of the unrolled
+// loop and each group's first MFMAs start from zero), or 0 (read from the arguments).
+template <int BK, bool GRP, int GPB = 0>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   constexpr int PF = GRP ? kPfGrouped : kPf;
+  static_assert(GPB == 0 || (GRP && kUnroll % GPB == 0), "compile-time groups divide the unroll");
   // With scale groups the tile is 256 x 64: each wave keeps two of the four interleaved MFMA
   // column sets (columns 4*cg + 2*wc + c, c = 0, 1), which halves both accumulator sets so that
   // the second one fits beside the operands without spilling.
@@ -344,12 +347,14 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) B[c] = *(const u32x4_v*)(bp + ((c_base + c) ^ b_par) * (kBK * 2));
   };
-  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[NC]) __attribute__((always_inline)) {
+  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[NC], auto first) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        if constexpr (GRP)
+        if constexpr (GRP && decltype(first)::value)
+          accg[rb][c] = mfma<BK>(A[rb], B[c], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        else if constexpr (GRP)
           accg[rb][c] = mfma<BK>(A[rb], B[c], accg[rb][c]);
         else
           acc[rb][c] = mfma<BK>(A[rb], B[c], acc[rb][c]);
@@ -363,7 +368,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       for (int c = 0; c < NC; ++c) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[rb][c][r] = __builtin_fmaf(accg[rb][c][r], sg[c], acc[rb][c][r]);
-        accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if constexpr (GPB == 0) accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     load_sg(g + 1);
   };
@@ -387,7 +392,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     read_step(B, 1, A1, B1);
     store_x(xr[S1], B ^ 1);
     store_w(wr4[S1], B ^ 1);
-    mma_step(A0, B0);
+    mma_step(A0, B0, std::integral_constant<bool, GPB != 0 && U % (GPB ? GPB : 1) == 0>{});
 #pragma unroll
     for (int i = 0; i < 2 * NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
@@ -406,7 +411,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     read_step(B ^ 1, 0, A0, B0);
     load_x(kb + PF, xr[S]);
     load_w(kb + PF, wr4[S]);
-    mma_step(A1, B1);
+    mma_step(A1, B1, std::false_type{});
 #pragma unroll
     for (int i = 0; i < 2 * NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
@@ -418,7 +423,9 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (GRP) {
+    if constexpr (GRP && GPB != 0) {
+      if constexpr ((U + 1) % (GPB ? GPB : 1) == 0) fold(kb / GPB);
+    } else if constexpr (GRP) {
       if ((kb + 1) % a.gpb == 0) fold(kb / a.gpb);
     }
   };
@@ -554,19 +561,23 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   return launch(b, name, [&] {
     switch (d.w_dt) {
       case MX_DTYPE_INT8:
-        grouped ? dispatch(qdense_gemm_kernel<kBI8, true>, grid, kThreads, 0, st, ga)
+        grouped ? (ga.gpb == 2 ? dispatch(qdense_gemm_kernel<kBI8, true, 2>, grid, kThreads, 0, st, ga)
+                               : dispatch(qdense_gemm_kernel<kBI8, true>, grid, kThreads, 0, st, ga))
                 : dispatch(qdense_gemm_kernel<kBI8, false>, grid, kThreads, 0, st, ga);
         break;
       case MX_DTYPE_UINT8:
-        grouped ? dispatch(qdense_gemm_kernel<kBU8, true>, grid, kThreads, 0, st, ga)
+        grouped ? (ga.gpb == 2 ? dispatch(qdense_gemm_kernel<kBU8, true, 2>, grid, kThreads, 0, st, ga)
+                               : dispatch(qdense_gemm_kernel<kBU8, true>, grid, kThreads, 0, st, ga))
                 : dispatch(qdense_gemm_kernel<kBU8, false>, grid, kThreads, 0, st, ga);
         break;
       case MX_DTYPE_INT4:
-        grouped ? dispatch(qdense_gemm_kernel<kBI4, true>, grid, kThreads, 0, st, ga)
+        grouped ? (ga.gpb == 2 ? dispatch(qdense_gemm_kernel<kBI4, true, 2>, grid, kThreads, 0, st, ga)
+                               : dispatch(qdense_gemm_kernel<kBI4, true>, grid, kThreads, 0, st, ga))
                 : dispatch(qdense_gemm_kernel<kBI4, false>, grid, kThreads, 0, st, ga);
         break;
       default:
-        grouped ? dispatch(qdense_gemm_kernel<kBU4, true>, grid, kThreads, 0, st, ga)
+        grouped ? (ga.gpb == 2 ? dispatch(qdense_gemm_kernel<kBU4, true, 2>, grid, kThreads, 0, st, ga)
+                               : dispatch(qdense_gemm_kernel<kBU4, true>, grid, kThreads, 0, st, ga))
                 : dispatch(qdense_gemm_kernel<kBU4, false>, grid, kThreads, 0, st, ga);
         break;
     }
