@@ -114,7 +114,7 @@ struct mx_backend {
   bool no_fusion = false;  // "nofusion" option: compile graphs op by op
   // "exact" option: FusedQuantizedDense always in the reference's loop order (bit-identical to it)
   bool exact_qdense = false;
-  bool gemv_over_gemm = false;  // measurement option: rows 17..64 stay on the GEMV where the GEMM fits
+  bool gemv_over_gemm = false;  // measurement option: rows 17..64 stay on the GEMV where the skinny row groups or the GEMM fit
   bool finalized = false;
   hipStream_t stream = nullptr;
   std::recursive_mutex mu;

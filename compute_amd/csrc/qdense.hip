@@ -418,7 +418,23 @@ static int qdense_dequant_run(mx_backend* b, const QDenseDesc& d, const char* na
 // =============================================================================================
 // Kernel selection.
 // =============================================================================================
-enum class QPath { kEmpty, kExact, kSkinny, kGemv, kGemm, kDequant };
+enum class QPath { kEmpty, kExact, kSkinny, kSkinnyRows, kGemv, kGemm, kDequant };
+
+// Past 16 rows of bf16 x: the skinny kernel once per group of 16 rows (its row limit).  Each
+// launch streams the weights once at decode rate (13-17 us per 16 rows at [4096] x 11008-14336
+// columns), while the GEMM's 256-row tiles are mostly padding at these M and its 128- or
+// 64-column tiles leave most CUs without work: one GEMM launch costs about 51 us there with
+// per-channel scales and 71-102 us with scale groups, so up to 3 (per-channel) or 4 (grouped)
+// skinny launches cost less.
+constexpr int64_t kSkinnyRowsPerLaunch = 16;
+
+static bool skinny_rows_fit(const QDenseDesc& d) {
+  const int64_t launches = d.block_size < d.K ? 4 : 3;
+  if (d.M <= kSkinnyRowsPerLaunch || d.M > launches * kSkinnyRowsPerLaunch) return false;
+  QDenseDesc g = d;
+  g.M = kSkinnyRowsPerLaunch;
+  return qdense_skinny_fits(g);
+}
 
 static GgmlDesc ggml_desc(const QDenseDesc& d) {
   GgmlDesc g;
@@ -439,6 +455,7 @@ static QPath choose_path(const mx_backend* b, const QDenseDesc& d) {
   if (d.M == 0 || d.N == 0) return QPath::kEmpty;
   if (d.scheme == MX_QUANT_GGML || b->exact_qdense) return QPath::kExact;
   if (qdense_skinny_fits(d)) return QPath::kSkinny;
+  if (!b->gemv_over_gemm && skinny_rows_fit(d)) return QPath::kSkinnyRows;
   // Past the skinny kernel's 16 rows the GEMM reads every weight once, while the GEMV reads the
   // whole weight matrix again for every 4 rows: the GEMV takes only what the GEMM does not fit.
   if (!b->gemv_over_gemm && qdense_gemm_fits(d)) return QPath::kGemm;
@@ -468,6 +485,13 @@ static const char* path_name(const QDenseDesc& d, QPath p) {
         case MX_DTYPE_INT8: return "qdense_skinny_mfma_i8";
         default: return "qdense_skinny_mfma_u8";
       }
+    case QPath::kSkinnyRows:
+      switch (d.w_dt) {
+        case MX_DTYPE_INT4: return "qdense_skinny_rows16_i4";
+        case MX_DTYPE_UINT4: return "qdense_skinny_rows16_u4";
+        case MX_DTYPE_INT8: return "qdense_skinny_rows16_i8";
+        default: return "qdense_skinny_rows16_u8";
+      }
     case QPath::kGemv:
       if (d.scheme == MX_QUANT_NF4) return dtype_is_packed(d.w_dt) ? "qdense_gemv_nf4_4bit" : "qdense_gemv_nf4_8bit";
       switch (d.w_dt) {
@@ -487,14 +511,14 @@ int qdense_plan_name(mx_backend* b, const QDenseDesc& d, std::string* name) {
   }
   const QPath p = choose_path(b, d);
   *name = path_name(d, p);
-  if (d.pair) *name += p == QPath::kSkinny ? "_pair" : "+" + *name + "+mul";
+  if (d.pair) *name += p == QPath::kSkinny || p == QPath::kSkinnyRows ? "_pair" : "+" + *name + "+mul";
   return MX_OK;
 }
 
 int qdense_run(mx_backend* b, const QDenseDesc& d) {
   MX_TRY(check_device(b));
   const QPath p = choose_path(b, d);
-  if (d.pair && p != QPath::kSkinny && p != QPath::kEmpty) {
+  if (d.pair && p != QPath::kSkinny && p != QPath::kSkinnyRows && p != QPath::kEmpty) {
     // Only the skinny kernel computes a pair in one launch: elsewhere the second product goes to
     // a temporary and the first applies the product in its epilogue (the same arithmetic).
     const size_t bytes = (size_t)d.M * d.N * (d.x_dt == MX_DTYPE_BFLOAT16 ? 2 : 4);
@@ -520,7 +544,7 @@ int qdense_run(mx_backend* b, const QDenseDesc& d) {
     dev_free(b, tmp);  // stream-ordered pool: later users run after these kernels
     return rc;
   }
-  if (d.res_op != 0 && p != QPath::kSkinny && p != QPath::kEmpty) {
+  if (d.res_op != 0 && p != QPath::kSkinny && p != QPath::kSkinnyRows && p != QPath::kEmpty) {
     // Only the skinny kernel applies a folded elementwise op in its epilogue: elsewhere the dense
     // result goes to a temporary and the op runs as its own kernel (the same arithmetic).
     const int64_t dims[2] = {d.M, d.N};
@@ -544,6 +568,19 @@ int qdense_run(mx_backend* b, const QDenseDesc& d) {
       return MX_OK;
     case QPath::kSkinny:
       return qdense_skinny_run(b, d, name);
+    case QPath::kSkinnyRows: {
+      // bf16 x and output; the elementwise operand has the output's shape.
+      const int64_t re = d.res ? dtype_bits(d.res_dt) / 8 : 0;
+      for (int64_t m0 = 0; m0 < d.M; m0 += kSkinnyRowsPerLaunch) {
+        QDenseDesc g = d;
+        g.M = std::min<int64_t>(kSkinnyRowsPerLaunch, d.M - m0);
+        g.x = (const char*)d.x + m0 * d.K * 2;
+        g.out = (char*)d.out + m0 * d.N * 2;
+        if (d.res) g.res = (const char*)d.res + m0 * d.N * re;
+        MX_TRY(qdense_skinny_run(b, g, name));
+      }
+      return MX_OK;
+    }
     case QPath::kGemv:
       return qdense_gemv_run(b, d, name);
     case QPath::kGemm:

@@ -306,13 +306,19 @@ def test_qdense_plan_selection():
                          block_size=4096) == want("qdense_gemv_i4")
             assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
                          block_size=4096) == want("qdense_gemm_mfma_i8")
-            # Past the skinny kernel's 16 rows, bf16 x with per-channel int8/uint8 takes the GEMM
-            # (weights read once) rather than the GEMV (weights re-read for every 4 rows).
-            for M in (17, 32, 64):
+            # Past the skinny kernel's 16 rows, bf16 x runs the skinny kernel once per group of 16
+            # rows up to 48 rows (per-channel scales) or 64 (scale groups), then the GEMM (weights
+            # read once); never the GEMV (weights re-read for every 4 rows).
+            for M, per_channel, grouped in ((17, "skinny_rows16", "skinny_rows16"), (48, "skinny_rows16", "skinny_rows16"),
+                                            (49, "gemm_mfma", "skinny_rows16"), (64, "gemm_mfma", "skinny_rows16"),
+                                            (65, "gemm_mfma", "gemm_mfma")):
                 assert _plan(b, M, 4096, 11008, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
-                             block_size=4096) == want("qdense_gemm_mfma_i8")
+                             block_size=4096) == want(f"qdense_{per_channel}_i8")
                 assert _plan(b, M, 4096, 11008, x_dtype=BF16, w_dtype=ca.Uint8, s_dtype=BF16, block_axis=0,
-                             block_size=4096) == want("qdense_gemm_mfma_u8")
+                             block_size=4096) == want(f"qdense_{per_channel}_u8")
+                sfx = "_grouped" if grouped == "gemm_mfma" else ""
+                assert _plan(b, M, 4096, 14336, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
+                             block_size=128) == want(f"qdense_{grouped}_i4{sfx}")
             # Where the GEMM does not fit (f32 x here), rows up to 64 stay on the GEMV.
             assert _plan(b, 32, 4096, 11008, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
                          block_size=64) == want("qdense_gemv_i8")

@@ -38,13 +38,13 @@ def test_nofusion_option():
         b.Finalize()
 
 
-def _qd_graph(backend, extra_use: bool, op: str = "add", res_first: bool = False, x_dtype=BFloat16):
+def _qd_graph(backend, extra_use: bool, op: str = "add", res_first: bool = False, x_dtype=BFloat16, M=2):
     bld = backend.Builder("qd_res")
     f = bld.Main()
-    x = f.Parameter("x", Shape(x_dtype, 2, 64))
+    x = f.Parameter("x", Shape(x_dtype, M, 64))
     w = f.Parameter("w", Shape(Int8, 64, 32))
     s = f.Parameter("s", Shape(Float32, 32))
-    r = f.Parameter("r", Shape(x_dtype, 2, 32))
+    r = f.Parameter("r", Shape(x_dtype, M, 32))
     y = f.FusedQuantizedDense(x, w, None, B.Quantization(B.QuantLinear, s, None, 0, 64), B.ActivationRelu)
     fn = f.Add if op == "add" else f.Mul
     z = fn(r, y) if res_first else fn(y, r)
@@ -115,24 +115,26 @@ def test_rmsnorm_small_rows_equal_unfused(backend, M):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("x_dtype,op,res_first", [(BFloat16, "add", False), (BFloat16, "mul", True),
-                                                  (Float32, "add", True), (Float32, "mul", False)])
-def test_dense_epilogue_equals_unfused(backend, x_dtype, op, res_first):
-    """bf16 x takes the skinny kernel (epilogue in the kernel); f32 x the exact kernel (dense
-    result to a temporary, then the elementwise kernel)."""
+@pytest.mark.parametrize("x_dtype,op,res_first,M", [(BFloat16, "add", False, 2), (BFloat16, "mul", True, 2),
+                                                    (Float32, "add", True, 2), (Float32, "mul", False, 2),
+                                                    (BFloat16, "add", True, 40), (BFloat16, "mul", False, 24)])
+def test_dense_epilogue_equals_unfused(backend, x_dtype, op, res_first, M):
+    """bf16 x takes the skinny kernel (epilogue in the kernel; past 16 rows once per group of 16
+    rows, the operand's rows offset with the output's); f32 x the exact kernel (dense result to a
+    temporary, then the elementwise kernel)."""
     rng = np.random.default_rng(7)
-    xs = rng.standard_normal((2, 64)).astype(np.float32)
-    rs = rng.standard_normal((2, 32)).astype(np.float32)
+    xs = rng.standard_normal((M, 64)).astype(np.float32)
+    rs = rng.standard_normal((M, 32)).astype(np.float32)
     x = bf16_from_f32(xs) if x_dtype == BFloat16 else xs
     r = bf16_from_f32(rs) if x_dtype == BFloat16 else rs
     w = rng.integers(-127, 128, (64, 32)).astype(np.int8)
     s = rng.uniform(0.01, 0.05, 32).astype(np.float32)
-    shapes = [Shape(x_dtype, 2, 64), Shape(Int8, 64, 32), Shape(Float32, 32), Shape(x_dtype, 2, 32)]
+    shapes = [Shape(x_dtype, M, 64), Shape(Int8, 64, 32), Shape(Float32, 32), Shape(x_dtype, M, 32)]
     nf = ca.New("nofusion")
     try:
         outs = []
         for b in (backend, nf):
-            e = _qd_graph(b, False, op, res_first, x_dtype)
+            e = _qd_graph(b, False, op, res_first, x_dtype, M)
             bufs = [b.BufferFromFlatData(0, d, sh) for d, sh in zip([x, w, s, r], shapes)]
             outs.append(e.Execute(bufs)[0].ToFlatData())
     finally:
@@ -213,6 +215,7 @@ PAIR_CASES = [
     (16, 2048, 384, Int8, 64, True, True, BFloat16),     # int8 g64, both biases
     (5, 512, 160, Uint8, 512, False, True, BFloat16),    # S = 1, ragged column block
     (4, 256, 64, Int8, 64, True, True, Float32),         # f32 x: exact kernels, pair fallback
+    (40, 1024, 512, Int4, 128, True, False, BFloat16),   # 40 rows: one pair launch per 16 rows
 ]
 
 

@@ -1,5 +1,6 @@
-"""Skinny-M FusedQuantizedDense (decode and small batches, M <= 16 bf16 rows) on the GPU vs the
-CPU oracle.
+"""Skinny-M FusedQuantizedDense (decode and small batches, M <= 16 bf16 rows, and once per group
+of 16 rows up to 48 rows with per-channel scales or 64 with scale groups) on the GPU vs the CPU
+oracle.
 
 The kernel sums in another order than the reference loop (per-group partial sums on the matrix
 cores, the group scale applied once per group, split-K partials added in slice order), so:
@@ -9,6 +10,8 @@ cores, the group scale applied once per group, split-K partials added in slice o
     top);
   - two calls on the same inputs must return identical bits (deterministic reduction).
 """
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -119,6 +122,29 @@ def test_skinny_partitions(backend, shape, w_dtype):
     r = QDenseRun(backend, p)
     assert r.plan().startswith("qdense_skinny_mfma")
     check(r, threads=8, what=f"{shape} {w_dtype}")
+
+
+SUFFIX = {O.DT_INT8: "i8", O.DT_UINT8: "u8", O.DT_INT4: "i4", O.DT_UINT4: "u4"}
+
+
+@pytest.mark.parametrize("M,w_dtype,G", [(17, O.DT_INT8, None), (33, O.DT_UINT8, None), (48, O.DT_INT8, None),
+                                         (40, O.DT_INT4, 128), (64, O.DT_INT8, 64), (23, O.DT_UINT4, 64)])
+def test_skinny_row_groups(backend, M, w_dtype, G):
+    """Past 16 rows: one launch per group of 16 rows, each launch the one a problem of just those
+    rows makes (the split and summation order depend on K and N only), so the rows of a group are
+    bit-identical to that problem's output."""
+    K, N = 1024, 2048
+    p = O.make_problem(M, K, N, w_dtype=w_dtype, block_axis=0, block_size=G if G else K, per_channel_1d=G is None,
+                       scale_dtype=O.DT_BFLOAT16 if G else O.DT_FLOAT32, bias=True, act=O.ACT_NONE,
+                       scale_range=(0.002, 0.02), seed=M)
+    r = QDenseRun(backend, p)
+    assert r.plan() == "qdense_skinny_rows16_" + SUFFIX[w_dtype]
+    y = check(r, threads=8, what=f"M={M} w={w_dtype} G={G}")
+    hi = min(32, M)  # the second group of rows
+    sub = dataclasses.replace(p, M=hi - 16, x=np.ascontiguousarray(p.x[16:hi]))
+    r16 = QDenseRun(backend, sub)
+    assert r16.plan() == "qdense_skinny_mfma_" + SUFFIX[w_dtype]
+    assert np.array_equal(r16.run(), y[16:hi])
 
 
 def test_skinny_shape_sequence(backend):

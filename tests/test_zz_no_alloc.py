@@ -81,15 +81,18 @@ SKINNY_I8 = [problem(16, 4096, 14336, 3, w_dtype=O.DT_INT8, block_axis=0, block_
                      scale_dtype=O.DT_FLOAT32)]
 GEMV = [problem(3, 4096, 2048, 5, w_dtype=O.DT_INT8, x_dtype=O.DT_FLOAT32, block_axis=0, block_size=64),
         problem(2, 1024, 1024, 6, w_dtype=O.DT_INT8, x_dtype=O.DT_FLOAT32, block_axis=0, block_size=64)]
-GEMM = [problem(32, 1024, 2048, 7, w_dtype=O.DT_INT8, block_axis=0, block_size=1024, per_channel_1d=True,
+GEMM = [problem(64, 1024, 2048, 7, w_dtype=O.DT_INT8, block_axis=0, block_size=1024, per_channel_1d=True,
                 scale_dtype=O.DT_FLOAT32),
-        problem(17, 512, 1024, 8, w_dtype=O.DT_INT8, block_axis=0, block_size=512, per_channel_1d=True,
+        problem(49, 512, 1024, 8, w_dtype=O.DT_INT8, block_axis=0, block_size=512, per_channel_1d=True,
                 scale_dtype=O.DT_FLOAT32)]
+SKINNY_ROWS = [problem(40, 4096, 2048, 12, w_dtype=O.DT_INT4, block_axis=0, block_size=128),
+               problem(20, 2048, 1024, 13, w_dtype=O.DT_INT4, block_axis=0, block_size=128)]
 
 
 @pytest.mark.parametrize("pair,plan", [(SKINNY, "qdense_skinny_mfma_i4"), (SKINNY_I8, "qdense_skinny_mfma_i8"),
-                                       (GEMV, "qdense_gemv_i8"), (GEMM, "qdense_gemm_mfma_i8")],
-                         ids=["skinny_i4", "skinny_i8", "gemv", "gemm"])
+                                       (SKINNY_ROWS, "qdense_skinny_rows16_i4"), (GEMV, "qdense_gemv_i8"),
+                                       (GEMM, "qdense_gemm_mfma_i8")],
+                         ids=["skinny_i4", "skinny_i8", "skinny_rows", "gemv", "gemm"])
 def test_noalloc_matches_qdense(backend, pair, plan):
     for p in pair:
         d = Direct(backend, p)
