@@ -11,14 +11,18 @@
 //   ggml_dense_exact — one output column per thread, k in order, every value dequantised and
 //                      every product and sum rounded as the reference rounds them: bit-identical
 //                      to the reference's f32 result.
-//   ggml_gemv<T, MR> — M <= 4 rows (decode): a wave per output column at a time, the column's row
-//                      of blocks staged through LDS with 16-byte loads (a row is contiguous), x in
+//   ggml_gemv<T, MR, CH, WV> — M <= 4 rows (decode), 8 or 16 waves: a wave per output column at a
+//                      time, the column's row of blocks staged through LDS with 16-byte loads (a
+//                      row is contiguous), x in
 //                      LDS as [m][32-value unit][36] (padded so that the 16 lanes of a 16-byte
 //                      read hit distinct banks).  Each lane takes 32-value units: their integer
 //                      codes times x are summed in f32 and the unit's scale (and min) applied
 //                      once, then the wave adds its lanes in a fixed tree.  f32 FMAs on the VALU:
 //                      x is f32 by contract, and bf16 matrix-core operands would not keep the
 //                      f32 accumulation bound.
+//   ggml_dequant_f32 — past 20 rows: a workgroup per row dequantises it (staged in LDS) to f32,
+//                      eight values per thread, for the f32 DotGeneral; ggml_epilogue then adds
+//                      the bias and applies the activation in place.
 //   ggml_embed       — one thread per output value (the reference's arithmetic, bit-identical);
 //                      indices of any integer dtype, bad indices reported after the launch.
 // Plans: up to 4 rows the GEMV; problems of at most 2^24 multiply-adds the exact kernel; up to 20
