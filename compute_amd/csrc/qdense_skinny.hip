@@ -38,8 +38,9 @@
 //               operand produces.
 //
 // Work decomposition.  The K steps of a column block are dealt out T at a time to waves, in
-// order; a workgroup of NW = 8 waves takes NW consecutive wave-chunks (one K slice), so a
-// column block has S = ceil(K/32 / (T*NW)) slices.  T is chosen per shape (the smallest even
+// order; a workgroup of NW = 8 waves (4 for one row when 8-wave workgroups would leave a quarter
+// of the CUs idle) takes NW consecutive wave-chunks (one K slice), so a column block has
+// S = ceil(K/32 / (T*NW)) slices.  T is chosen per shape (the smallest even
 // divisor of K/32 that keeps the grid within one workgroup per CU).  A wave folds a group's
 // partial sums into its total with the group's scale when the group ends, or at its last step.
 // The waves' partial tiles are summed through LDS in wave order; with S > 1 every workgroup
@@ -61,7 +62,6 @@ typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
 
 constexpr int kSkMaxRows = 16;
 constexpr int kSkWaves = 8;
-constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkLaneBytes = 8;  // bytes of one weight row per lane
 
 struct SkinnyArgs {
@@ -132,8 +132,11 @@ __device__ __forceinline__ float sk_value(SkWord v, const void* p, int dt) {
 // line it misses costs a trip to L2 or beyond.
 // G2: the scale groups are two steps (G = 64), so a group is exactly one loop iteration's pair:
 // its first step's MFMAs start from zero and its second folds, with no clearing of the sums.
-template <int WDT, int MR, bool SF32, bool PIPE, bool G2>
-__global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a) {
+// WV: waves per workgroup, 8, or 4 for single-row launches whose 8-wave grid would leave a
+// quarter of the CUs idle (twice the workgroups, two per CU).
+template <int WDT, int MR, bool SF32, bool PIPE, bool G2, int WV = kSkWaves>
+__global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(SkinnyArgs a) {
+  constexpr int kWv = WV, kThr = 64 * WV;
   constexpr bool kI4 = WDT == MX_DTYPE_INT4 || WDT == MX_DTYPE_UINT4;
   constexpr int CPL = kI4 ? 2 * kSkLaneBytes : kSkLaneBytes;  // columns per lane
   constexpr int kCols = 16 * CPL;                              // columns per workgroup
@@ -152,27 +155,27 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int cg = lane & 15, kq = lane >> 4;
   const int KS = a.K >> 5;
-  const int k0 = (slice * kSkWaves + wave) * a.T;  // first K step of this wave
+  const int k0 = (slice * kWv + wave) * a.T;  // first K step of this wave
   const int cblk = cb * kCols;
   const int col0 = cblk + cg * CPL;
 
   const int M = a.M;
   constexpr int kQPR = kCols / 4;  // quads per tile row
-  constexpr int kMaxQ = kSkMaxRows * kQPR / kSkThreads;  // quads per thread (M = 16)
+  constexpr int kMaxQ = kSkMaxRows * kQPR / kThr;  // quads per thread (M = 16)
   const int t = threadIdx.x;
   const int MC = M * kCols, NQ = M * kQPR;
   auto wave_sum = [&](int g) __attribute__((always_inline)) {
     f32x4_t y = *(const f32x4_t*)(red + 4 * g);
 #pragma unroll
-    for (int w = 1; w < kSkWaves; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
+    for (int w = 1; w < kWv; ++w) y += *(const f32x4_t*)(red + w * MC + 4 * g);
     return y;
   };
-  // The workgroup's tile of each product, summed over the waves (quad g = t + i * kSkThreads):
+  // The workgroup's tile of each product, summed over the waves (quad g = t + i * kThr):
   // the last product's stays as the waves' tiles in LDS, the first of a pair is summed into an
   // LDS tile of its own before the second is computed.
-  float* held = red + (size_t)kSkWaves * M * kCols;
+  float* held = red + (size_t)kWv * M * kCols;
   auto tile = [&](int mat, int i) __attribute__((always_inline)) {
-    const int g = min(t + i * kSkThreads, NQ - 1);
+    const int g = min(t + i * kThr, NQ - 1);
     return mat + 1 < NM ? *(const f32x4_t*)(held + 4 * g) : wave_sum(g);
   };
 #pragma unroll 1
@@ -373,7 +376,7 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
   if (mat + 1 < NM) {
 #pragma unroll
     for (int i = 0; i < kMaxQ; ++i) {
-      const int g = min(t + i * kSkThreads, NQ - 1);
+      const int g = min(t + i * kThr, NQ - 1);
       *(f32x4_t*)(held + 4 * g) = wave_sum(g);
     }
     __syncthreads();  // the waves' tiles are free for the next product
@@ -390,7 +393,7 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
     // Only the last arriver reads the tiles back, with loads that carry the same bit.
 #pragma unroll
     for (int i = 0; i < kMaxQ; ++i) {
-      const int g = t + i * kSkThreads;
+      const int g = t + i * kThr;
       const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
       if (g < NQ && col < a.N) {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, tile(0, i)), prs,
@@ -422,7 +425,7 @@ __global__ __launch_bounds__(kSkThreads) void qdense_skinny_kernel(SkinnyArgs a)
   const bool plain = a.act == MX_ACT_NONE && !a.pair && !a.res_op;
 #pragma unroll 1
   for (int i = 0; i < kMaxQ; ++i) {
-    const int g = t + i * kSkThreads;
+    const int g = t + i * kThr;
     const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
     if (g >= NQ || col >= a.N) continue;
     f32x4_t y, y2;
@@ -513,35 +516,51 @@ bool qdense_skinny_fits(const QDenseDesc& d) {
 }
 
 // Steps per wave T: 1 when K/32 is odd; else the smallest even divisor of K/32 whose grid (column
-// blocks x slices) is at most one workgroup per CU, so that the whole grid is resident at once
-// (the largest even divisor when none is).  T fixes the summation order, so it depends on the
-// shape of one product only: a pair launch sums each product exactly as its own launch would.
-static int skinny_steps(const QDenseDesc& d, int64_t nb, int num_cus) {
+// blocks x slices of `waves` wave-chunks) is within the resident workgroups (one per CU with 8
+// waves, two with 4), so that the whole grid is resident at once (the largest even divisor when
+// none is).  T and the wave count fix the summation order, so they depend on the shape of one
+// product only: a pair launch sums each product exactly as its own launch would.
+static int skinny_steps(const QDenseDesc& d, int64_t nb, int num_cus, int waves) {
   const int64_t ks = d.K / 32;
   if (ks % 2 != 0) return 1;
   int64_t best = 0;
   for (int64_t T = 2; T <= ks; T += 2) {
     if (ks % T != 0) continue;
     best = T;
-    const int64_t S = (ks / T + kSkWaves - 1) / kSkWaves;
-    if (nb * S <= num_cus) break;
+    const int64_t S = (ks / T + waves - 1) / waves;
+    if (nb * S <= (int64_t)num_cus * (kSkWaves / waves)) break;
   }
   return (int)best;
 }
 
-template <int WDT, int MR, bool SF32>
+// Waves per workgroup: 4 for one row when the 8-wave grid would fill at most three quarters of
+// the CUs (C2: 172 workgroups of 8 waves, 9.7-9.9 us as 344 of 4 against 10.1-10.4 us); 8
+// otherwise (batched shapes measured slower with 4: C3 18.1 -> 20.4 us, the MLP 41.5 -> 50.4 us).
+static int skinny_waves(const QDenseDesc& d, int64_t nb, int num_cus) {
+  if (d.M != 1) return kSkWaves;
+  const int64_t T8 = skinny_steps(d, nb, num_cus, kSkWaves);
+  const int64_t S8 = (d.K / 32 / T8 + kSkWaves - 1) / kSkWaves;
+  return 4 * nb * S8 <= 3 * (int64_t)num_cus ? 4 : kSkWaves;
+}
+
+template <int WDT, int MR, bool SF32, int WV = kSkWaves>
 static void launch_pipe(const SkinnyArgs& ga, int grid, size_t lds, hipStream_t st) {
   if (ga.T >= 2 && ga.FS == 2)
-    dispatch(qdense_skinny_kernel<WDT, MR, SF32, true, true>, grid, kSkThreads, lds, st, ga);
+    dispatch(qdense_skinny_kernel<WDT, MR, SF32, true, true, WV>, grid, 64 * WV, lds, st, ga);
   else if (ga.T >= 2)
-    dispatch(qdense_skinny_kernel<WDT, MR, SF32, true, false>, grid, kSkThreads, lds, st, ga);
+    dispatch(qdense_skinny_kernel<WDT, MR, SF32, true, false, WV>, grid, 64 * WV, lds, st, ga);
   else
-    dispatch(qdense_skinny_kernel<WDT, MR, SF32, false, false>, grid, kSkThreads, lds, st, ga);
+    dispatch(qdense_skinny_kernel<WDT, MR, SF32, false, false, WV>, grid, 64 * WV, lds, st, ga);
 }
 
 template <int WDT>
-static void launch_skinny(const SkinnyArgs& ga, bool sf32, int grid, size_t lds, hipStream_t st) {
-  if (ga.M == 1) {
+static void launch_skinny(const SkinnyArgs& ga, bool sf32, int waves, int grid, size_t lds, hipStream_t st) {
+  if (ga.M == 1 && waves == 4) {
+    if (sf32)
+      launch_pipe<WDT, 1, true, 4>(ga, grid, lds, st);
+    else
+      launch_pipe<WDT, 1, false, 4>(ga, grid, lds, st);
+  } else if (ga.M == 1) {
     if (sf32)
       launch_pipe<WDT, 1, true>(ga, grid, lds, st);
     else
@@ -558,9 +577,11 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   const bool i4 = dtype_is_packed(d.w_dt);
   const int64_t cols = i4 ? 256 : 128;
   const int64_t nb = (d.N + cols - 1) / cols;
-  const int T = skinny_steps(d, nb, b->num_cus > 0 ? b->num_cus : 256);
+  const int ncu = b->num_cus > 0 ? b->num_cus : 256;
+  const int waves = skinny_waves(d, nb, ncu);
+  const int T = skinny_steps(d, nb, ncu, waves);
   const int64_t chunks = d.K / 32 / T;  // wave-sized pieces of one column block
-  const int64_t S = (chunks + kSkWaves - 1) / kSkWaves;
+  const int64_t S = (chunks + waves - 1) / waves;
   const int64_t SP = d.pair ? 2 * S : S;  // partial tiles per column block
   const size_t counter_bytes = 64 * 1024;
   if ((size_t)nb * 4 > counter_bytes || nb * SP > (int64_t)1 << 30 || SP * d.M * d.N * 4 >= (int64_t)1 << 31)
@@ -598,15 +619,15 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.b2_dt = d.b2_dt;
   const int grid = (int)(nb * S);
   // LDS: the waves' tiles [waves][M][cols] and the first product's tile [M][cols].
-  const size_t lds = (size_t)(kSkWaves + 1) * d.M * cols * sizeof(float);
+  const size_t lds = (size_t)(waves + 1) * d.M * cols * sizeof(float);
   const bool sf32 = d.s_dt == MX_DTYPE_FLOAT32;
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     switch (d.w_dt) {
-      case MX_DTYPE_INT4: launch_skinny<MX_DTYPE_INT4>(ga, sf32, grid, lds, st); break;
-      case MX_DTYPE_UINT4: launch_skinny<MX_DTYPE_UINT4>(ga, sf32, grid, lds, st); break;
-      case MX_DTYPE_INT8: launch_skinny<MX_DTYPE_INT8>(ga, sf32, grid, lds, st); break;
-      default: launch_skinny<MX_DTYPE_UINT8>(ga, sf32, grid, lds, st); break;
+      case MX_DTYPE_INT4: launch_skinny<MX_DTYPE_INT4>(ga, sf32, waves, grid, lds, st); break;
+      case MX_DTYPE_UINT4: launch_skinny<MX_DTYPE_UINT4>(ga, sf32, waves, grid, lds, st); break;
+      case MX_DTYPE_INT8: launch_skinny<MX_DTYPE_INT8>(ga, sf32, waves, grid, lds, st); break;
+      default: launch_skinny<MX_DTYPE_UINT8>(ga, sf32, waves, grid, lds, st); break;
     }
   });
 }
