@@ -9,7 +9,8 @@ from .dtypes import (  # noqa: F401
 )
 from .backend import (  # noqa: F401
     ActivationGelu, ActivationHardSwish, ActivationNone, ActivationRelu, ActivationSilu, ActivationTanh,
-    ActivationType, Backend, Buffer, Builder, Capabilities, ComputeError, DotGeneralConfig, ErrFinalized,
+    ActivationType, Backend, Buffer, Builder, Capabilities, ComputeError, DenseConfig, DenseLayout,
+    DenseLayoutInputOutputs, DenseLayoutOutputsInput, DotGeneralConfig, ErrFinalized,
     ErrNoDevice, ErrNotImplemented, Executable, Function, IsNotImplemented, NF4LookupTable, New, OpType,
     QuantGGML, QuantLinear, QuantNF4, Quantization, QuantizationScheme, Value,
     GGMLQuantType, GGMLQ4_0, GGMLQ8_0, GGMLIQ4NL, GGMLQ2_K, GGMLQ3_K, GGMLQ4_K, GGMLQ5_K, GGMLQ6_K,

@@ -38,6 +38,10 @@ class mx_quantization(C.Structure):
     ]
 
 
+class mx_dense_config(C.Structure):
+    _fields_ = [("activation", C.c_int32), ("weight_layout", C.c_int32)]
+
+
 class mx_qdense_args(C.Structure):
     _fields_ = [
         ("x", C.c_void_p),
@@ -102,6 +106,7 @@ SIGNATURES = {
     "mx_backend_profile_entry": [_P, _I, C.c_char_p, _SZ, _I64P, C.POINTER(C.c_double)],
     "mx_backend_profile_reset": [_P],
     "mx_backend_debug_fail_alloc_after": [_P, _I],
+    "mx_backend_debug_noalloc_scratch": [_P, C.POINTER(_P)],
     "mx_backend_has_shared_buffers": [_P, C.POINTER(_I)],
     "mx_buffer_from_flat": [_P, _I, _P, _SZ, _SHP, C.POINTER(_P)],
     "mx_buffer_to_flat": [_P, _P, _SZ],
@@ -123,7 +128,7 @@ SIGNATURES = {
     "mx_fn_fused_quantized_dense": [_P, _VAL, _VAL, _VAL, C.POINTER(mx_quantization), _I, _VALP],
     "mx_fn_quantized_embedding_lookup": [_P, _VAL, _VAL, C.POINTER(mx_quantization), _VALP],
     "mx_fn_dot_general": [_P, _VAL, _I32P, _I, _I32P, _I, _VAL, _I32P, _I, _I32P, _I, _I, _I, _VALP],
-    "mx_fn_fused_dense": [_P, _VAL, _VAL, _VAL, _I, _VALP],
+    "mx_fn_fused_dense": [_P, _VAL, _VAL, _VAL, C.POINTER(mx_dense_config), _VALP],
     "mx_fn_fused_gelu": [_P, _VAL, _I, _VALP],
     "mx_fn_unary": [_P, _I, _VAL, _VALP],
     "mx_fn_binary": [_P, _I, _VAL, _VAL, _VALP],

@@ -175,6 +175,24 @@ class Quantization:
     GGMLType: int = 0
 
 
+class DenseLayout(enum.IntEnum):
+    """compute.DenseLayout (fused_ops.go:51-57)."""
+
+    DenseLayoutInputOutputs = 0
+    DenseLayoutOutputsInput = 1
+
+
+DenseLayoutInputOutputs, DenseLayoutOutputsInput = DenseLayout
+
+
+@dataclass
+class DenseConfig:
+    """compute.DenseConfig (fused_ops.go:73-77)."""
+
+    Activation: ActivationType = ActivationNone
+    WeightLayout: DenseLayout = DenseLayoutInputOutputs
+
+
 @dataclass
 class DotGeneralConfig:
     """compute.DotGeneralConfig (standard_ops.go:91-111)."""
@@ -354,6 +372,12 @@ class Backend:
     def DebugFailAllocAfter(self, n: int) -> None:
         _check(self._lib.mx_backend_debug_fail_alloc_after(self._h, n))
 
+    def DebugNoAllocScratch(self) -> int:
+        """Device address of the static array mx_qdense_noalloc uses on this backend's GPU."""
+        p = C.c_void_p()
+        _check(self._lib.mx_backend_debug_noalloc_scratch(self._h, C.byref(p)))
+        return int(p.value or 0)
+
     def __repr__(self) -> str:
         return f"Backend({self.Name()!r})"
 
@@ -532,8 +556,10 @@ class Function:
                                   int(q.BlockSize), int(q.GGMLType))
         return self._out(self._lib.mx_fn_quantized_embedding_lookup, int(data), int(indices), C.byref(cq))
 
-    def FusedDense(self, x: Value, weight: Value, bias: Optional[Value], activation=ActivationNone) -> Value:
-        return self._out(self._lib.mx_fn_fused_dense, int(x), int(weight), int(bias or 0), int(activation))
+    def FusedDense(self, x: Value, weight: Value, bias: Optional[Value], options: DenseConfig = None) -> Value:
+        o = options if options is not None else DenseConfig()
+        cfg = _lib.mx_dense_config(int(o.Activation), int(o.WeightLayout))
+        return self._out(self._lib.mx_fn_fused_dense, int(x), int(weight), int(bias or 0), C.byref(cfg))
 
     def FusedGelu(self, x: Value, exact: bool) -> Value:
         return self._out(self._lib.mx_fn_fused_gelu, int(x), int(bool(exact)))

@@ -737,26 +737,54 @@ int mx_fn_dot_general(mx_function* fn, mx_value lhsv, const int32_t* lc, int n_l
   return MX_OK;
 }
 
-// FusedDense (fused_ops.go:347; reference lowering fusedops/dense.go:34-163): DotGeneral of x's
-// last axis with weight's first axis, plus bias, plus activation.
-int mx_fn_fused_dense(mx_function* fn, mx_value xv, mx_value wv, mx_value biasv, int activation, mx_value* out) {
+// FusedDense (fused_ops.go:347, DenseConfig fused_ops.go:73-77; reference lowering
+// fusedops/dense.go:34-163): DotGeneral of x's last axis with the weight's first axis
+// (DenseLayoutInputOutputs, weight [in, out...]) or last axis (DenseLayoutOutputsInput, weight
+// [out..., in]), plus bias, plus activation.  Output dims: x's leading dims, then the weight's
+// output dims (dense.go:59-80).
+int mx_fn_fused_dense(mx_function* fn, mx_value xv, mx_value wv, mx_value biasv, const mx_dense_config* options,
+                      mx_value* out) {
   clear_error();
   const char* op = "FusedDense";
   MX_TRY(check_fn(fn, op));
+  const int activation = options ? options->activation : MX_ACT_NONE;
+  const int layout = options ? options->weight_layout : MX_DENSE_LAYOUT_INPUT_OUTPUTS;
   int x, w, bias = -1;
   MX_TRY(get_node(fn->bld, xv, op, &x));
   MX_TRY(get_node(fn->bld, wv, op, &w));
   if (biasv) MX_TRY(get_node(fn->bld, biasv, op, &bias));
   const Shape xs = shape_of(fn, x), ws = shape_of(fn, w);
   if (xs.rank() < 1 || ws.rank() < 2)
-    return set_error(MX_ERR_INVALID, "%s: x must have rank >= 1 and weight rank >= 2, got %s and %s", op,
-                     xs.str().c_str(), ws.str().c_str());
+    return set_error(MX_ERR_INVALID, "%s: x must have rank >= 1 (got %d), weight must have rank >= 2 (got %d)", op,
+                     xs.rank(), ws.rank());
+  const int64_t in_features = xs.dims[xs.rank() - 1];
+  int32_t rc0;
+  int64_t cols = 1;  // output features: the weight's dims other than the contracted one
+  if (layout == MX_DENSE_LAYOUT_INPUT_OUTPUTS) {
+    if (in_features != ws.dims[0])
+      return set_error(MX_ERR_INVALID,
+                       "%s: x's last dim (%lld) must match weight's first dim (%lld) for DenseLayoutInputOutputs", op,
+                       (long long)in_features, (long long)ws.dims[0]);
+    rc0 = 0;
+    for (int i = 1; i < ws.rank(); ++i) cols *= ws.dims[i];
+  } else if (layout == MX_DENSE_LAYOUT_OUTPUTS_INPUT) {
+    const int last = ws.rank() - 1;
+    if (in_features != ws.dims[last])
+      return set_error(MX_ERR_INVALID,
+                       "%s: x's last dim (%lld) must match weight's last dim (%lld) for DenseLayoutOutputsInput", op,
+                       (long long)in_features, (long long)ws.dims[last]);
+    rc0 = last;
+    for (int i = 0; i < last; ++i) cols *= ws.dims[i];
+  } else {
+    // The reference formats the layout with %v, which prints DenseLayout.String(): "unknown".
+    return set_error(MX_ERR_INVALID, "%s: unknown WeightLayout unknown", op);
+  }
   if (activation < MX_ACT_NONE || activation > MX_ACT_TANH)
     return set_error(MX_ERR_INVALID, "%s: unknown activation %d", op, activation);
   if (xs.dtype != MX_DTYPE_FLOAT32 && xs.dtype != MX_DTYPE_FLOAT64 && xs.dtype != MX_DTYPE_BFLOAT16)
     return set_error(MX_ERR_NOT_IMPLEMENTED, "%s: dtype %s", op, dtype_name(xs.dtype));
   const size_t before = fn->bld->fn.nodes.size();
-  int32_t lc = xs.rank() - 1, rc0 = 0;
+  int32_t lc = xs.rank() - 1;
   int y;
   int rc_ = dot_general_idx(fn, x, &lc, 1, nullptr, 0, w, &rc0, 1, nullptr, 0, MX_DTYPE_INVALID, MX_DTYPE_INVALID, &y);
   if (rc_ != MX_OK) {
@@ -764,8 +792,6 @@ int mx_fn_fused_dense(mx_function* fn, mx_value xv, mx_value wv, mx_value biasv,
     return rc_;
   }
   const Shape ys = shape_of(fn, y);
-  int64_t cols = 1;
-  for (int i = 1; i < ws.rank(); ++i) cols *= ws.dims[i];
   if (bias >= 0) {
     const Shape bs = shape_of(fn, bias);
     if (bs.dtype != xs.dtype || bs.size() != cols) {

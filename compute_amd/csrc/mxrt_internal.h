@@ -133,6 +133,7 @@ struct mx_backend {
   // whether such a call is in progress: then scratch comes from that array and nothing may
   // allocate device memory.
   void* noalloc_scratch = nullptr;
+  void* noalloc_order = nullptr;  // the device's call-ordering state (qdense_noalloc.hip)
   bool noalloc_active = false;
 
   // Profiling.

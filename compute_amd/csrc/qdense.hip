@@ -52,7 +52,7 @@ static int ggml_validate(const mx_qdense_args* a, QDenseDesc* d) {
   if (a->M < 0 || a->K < 0 || a->N < 0 || a->K % vpb != 0)
     return set_error(MX_ERR_INVALID, "%s: K=%lld must be a non-negative multiple of %d (M=%lld, N=%lld)", op,
                      (long long)a->K, vpb, (long long)a->M, (long long)a->N);
-  if (a->K > (int64_t)1 << 31 || a->N > (int64_t)1 << 31) return set_error(MX_ERR_INVALID, "%s: K and N must be < 2^31", op);
+  if (a->K >= (int64_t)1 << 31 || a->N >= (int64_t)1 << 31) return set_error(MX_ERR_INVALID, "%s: K and N must be < 2^31", op);
   if (a->M * a->N > 0 && (!a->out || (a->K > 0 && (!a->x || !a->w))))
     return set_error(MX_ERR_INVALID, "%s: NULL data pointer", op);
   *d = QDenseDesc{};
@@ -97,8 +97,17 @@ int qdense_validate(const mx_qdense_args* a, QDenseDesc* d) {
   if (a->M < 0 || a->K < 0 || a->N < 0)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: negative size M=%lld K=%lld N=%lld",
                      (long long)a->M, (long long)a->K, (long long)a->N);
-  if (a->K > (int64_t)1 << 31 || a->N > (int64_t)1 << 31)
+  if (a->K >= (int64_t)1 << 31 || a->N >= (int64_t)1 << 31)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: K and N must be < 2^31");
+  // Element alignment (what a Go slice of the dtype always has): f32 on 4 bytes, bf16 on 2.
+  auto misaligned = [](const void* p, int dt) {
+    return p && ((uintptr_t)p % (uintptr_t)(dt == MX_DTYPE_FLOAT32 ? 4 : 2)) != 0;
+  };
+  if (misaligned(a->x, a->x_dtype) || misaligned(a->scale, a->scale_dtype) ||
+      (a->zero_point && misaligned(a->zero_point, a->zero_point_dtype)) ||
+      (a->bias && misaligned(a->bias, a->bias_dtype)) || misaligned(a->out, a->x_dtype))
+    return set_error(MX_ERR_INVALID,
+                     "FusedQuantizedDense: float32 data must be 4-byte aligned and bfloat16 data 2-byte aligned");
   int64_t outs = a->M * a->N;
   if (outs > 0 && (!a->out || (a->K > 0 && (!a->x || !a->w || !a->scale))))
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: NULL data pointer");
@@ -134,11 +143,17 @@ constexpr int kExactU = 16;    // k per batch of weight / scale requests (see U)
 //   - a bf16 or f32 element (scales, zero points) is read as the aligned 32-bit word holding it
 //     and shifted into f32 position (bf16 widened exactly).
 // Element indices advance by a constant per k: no multiplication or division per k.
+// The word is the aligned one that holds the element's absolute address (bf16 arrays need only be
+// 2-byte aligned), so the load never leaves the element's own 4 bytes.
 __device__ __forceinline__ uint32_t word_of(const void* p, uint64_t i, int sh) {
-  return *(const uint32_t*)((const char*)p + ((i << sh) & ~(uint64_t)3));
+  return *(const uint32_t*)(((uintptr_t)p + (i << sh)) & ~(uintptr_t)3);
 }
-// The f32 value of element i from its word: f32 (sh 2) as is, bf16 (sh 1) moved to the high half.
-__device__ __forceinline__ uint32_t word_shift(uint64_t i, int sh) { return sh == 2 || (i & 1) ? 0u : 16u; }
+// The f32 value of element i from its word: f32 (sh 2) as is, bf16 (sh 1) moved to the high half
+// when it sits in the word's low half.  podd: bit 1 of the array's address (an array that starts
+// 2 bytes into a word has its even elements in high halves).
+__device__ __forceinline__ uint32_t word_shift(uint64_t i, int sh, uint32_t podd) {
+  return sh == 2 || ((i ^ podd) & 1) ? 0u : 16u;
+}
 __device__ __forceinline__ float word_value(uint32_t w, uint32_t shift, uint32_t mask) {
   return __uint_as_float((w << shift) & mask);
 }
@@ -164,6 +179,7 @@ __global__ __launch_bounds__(kExactThreads) void qdense_exact_kernel(QDenseDesc 
   const uint32_t wbits = packed ? 4u : 8u, wsh = packed ? 1u : 0u;
   const int s_sh = d.s_dt == MX_DTYPE_BFLOAT16 ? 1 : 2, z_sh = d.zp_dt == MX_DTYPE_BFLOAT16 ? 1 : 2;
   const uint32_t s_mask = s_sh == 2 ? ~0u : 0xFFFF0000u, z_mask = z_sh == 2 ? ~0u : 0xFFFF0000u;
+  const uint32_t s_odd = (uint32_t)((uintptr_t)d.scale >> 1) & 1u, z_odd = (uint32_t)((uintptr_t)d.zp >> 1) & 1u;
   const bool nf = d.scheme == MX_QUANT_NF4;
   if (threadIdx.x < 16) nf4[threadIdx.x] = kNF4Table[threadIdx.x];
   // Scale (and zero point) of row k: block_axis 1 (reference layout, [K, ceil(N/B)]) at
@@ -174,8 +190,9 @@ __global__ __launch_bounds__(kExactThreads) void qdense_exact_kernel(QDenseDesc 
   const int64_t scol = ax1 ? (int64_t)((uint32_t)nn / (uint32_t)B) : nn;
   float s_col = 0.0f, z_col = 0.0f;  // one scale per column (SK false)
   if constexpr (!SK) {
-    s_col = word_value(word_of(d.scale, (uint64_t)scol, s_sh), word_shift((uint64_t)scol, s_sh), s_mask);
-    if constexpr (ZP) z_col = word_value(word_of(d.zp, (uint64_t)scol, z_sh), word_shift((uint64_t)scol, z_sh), z_mask);
+    s_col = word_value(word_of(d.scale, (uint64_t)scol, s_sh), word_shift((uint64_t)scol, s_sh, s_odd), s_mask);
+    if constexpr (ZP)
+      z_col = word_value(word_of(d.zp, (uint64_t)scol, z_sh), word_shift((uint64_t)scol, z_sh, z_odd), z_mask);
   }
   float acc[R];
   const float b0 = d.bias ? load_f(d.bias, nn, d.b_dt) : 0.0f;
@@ -222,10 +239,10 @@ __global__ __launch_bounds__(kExactThreads) void qdense_exact_kernel(QDenseDesc 
       bt.w[j] = ((const uint8_t*)d.w)[wi >> wsh];
       if constexpr (SK) {
         bt.s[j] = word_of(d.scale, si, s_sh);
-        bt.ssh[j] = word_shift(si, s_sh);
+        bt.ssh[j] = word_shift(si, s_sh, s_odd);
         if constexpr (ZP) {
           bt.z[j] = word_of(d.zp, si, z_sh);
-          bt.zsh[j] = word_shift(si, z_sh);
+          bt.zsh[j] = word_shift(si, z_sh, z_odd);
         }
       }
       if (FULL || k0 + j + 1 < kend) {

@@ -17,7 +17,14 @@
 // once per device, here, at set-up; the partial tiles are written before they are read.
 //
 // Every call on one GPU shares that GPU's array, from any backend, and the array keeps the last
-// call's contents: calls that overlap on one GPU (several streams or backends) race.
+// call's contents.  Calls are therefore ordered on the device: each call's stream first waits
+// for the previous call's completion event (recorded on whichever stream that call used), then
+// launches, then records the event again, all under a per-device lock.  Calls from several
+// streams or backends thus run one after another without allocating.  A stream under graph
+// capture is the exception: capture cannot wait on an event recorded outside the graph, so a
+// captured call is ordered only by the caller; a captured graph replayed while another noalloc
+// call runs on the same GPU races with it, and the counters it disturbs can then make later calls
+// on that GPU wrong as well.
 #include <map>
 #include <mutex>
 
@@ -35,6 +42,14 @@ static_assert(MX_QDENSE_NOALLOC_SCRATCH_BYTES > kCounterBytes, "scratch holds th
 std::mutex g_mu;
 std::map<int, void*> g_scratch_ptr;  // device -> that device's address of `scratch`
 
+// Per-device ordering of the calls that share `scratch`.
+struct Order {
+  std::mutex mu;
+  hipEvent_t done = nullptr;  // completion of the last call (valid once `used`)
+  bool used = false;
+};
+std::map<int, Order*> g_order;  // device -> ordering state (created at set-up, never freed)
+
 __global__ void clear_words(uint32_t* p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0u;
@@ -47,7 +62,14 @@ int noalloc_scratch_setup(mx_backend* b) {
   auto it = g_scratch_ptr.find(b->device);
   if (it != g_scratch_ptr.end()) {
     b->noalloc_scratch = it->second;
+    b->noalloc_order = g_order[b->device];
     return MX_OK;
+  }
+  Order* ord = new Order;
+  if (hipError_t ee = hipEventCreateWithFlags(&ord->done, hipEventDisableTiming); ee != hipSuccess) {
+    delete ord;
+    return set_error(MX_ERR_HIP, "hipEventCreate for mx_qdense_noalloc on device %d failed: %s", b->device,
+                     hipGetErrorString(ee));
   }
   void* ptr = nullptr;
   hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
@@ -61,7 +83,9 @@ int noalloc_scratch_setup(mx_backend* b) {
   MX_CHECK_HIP(hipGetLastError());
   MX_CHECK_HIP(hipStreamSynchronize(b->stream));
   g_scratch_ptr[b->device] = ptr;
+  g_order[b->device] = ord;
   b->noalloc_scratch = ptr;
+  b->noalloc_order = ord;
   return MX_OK;
 }
 
@@ -75,10 +99,38 @@ extern "C" int mx_qdense_noalloc(mx_backend* b, const mx_qdense_args* args) {
   mx::QDenseDesc d;
   MX_TRY(mx::qdense_validate(args, &d));
   std::lock_guard<std::recursive_mutex> lk(b->mu);
-  struct Scope {
-    mx_backend* b;
-    explicit Scope(mx_backend* bb) : b(bb) { b->noalloc_active = true; }
-    ~Scope() { b->noalloc_active = false; }
-  } scope(b);
-  return mx::qdense_run(b, d);
+  auto* ord = static_cast<mx::Order*>(b->noalloc_order);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  MX_CHECK_HIP(hipStreamIsCapturing(b->stream, &cs));
+  const bool ordered = cs == hipStreamCaptureStatusNone;
+  std::unique_lock<std::mutex> olk(ord->mu, std::defer_lock);
+  if (ordered) {
+    olk.lock();
+    // Wait for the previous call on this GPU, from any stream or backend (a no-op when it was
+    // on this stream, whose order already holds).
+    if (ord->used) MX_CHECK_HIP(hipStreamWaitEvent(b->stream, ord->done, 0));
+  }
+  int rc;
+  {
+    struct Scope {
+      mx_backend* b;
+      explicit Scope(mx_backend* bb) : b(bb) { b->noalloc_active = true; }
+      ~Scope() { b->noalloc_active = false; }
+    } scope(b);
+    rc = mx::qdense_run(b, d);
+  }
+  if (ordered) {
+    // Recorded even after a failed launch, so that the next call still waits for whatever this
+    // one queued.
+    MX_CHECK_HIP(hipEventRecord(ord->done, b->stream));
+    ord->used = true;
+  }
+  return rc;
+}
+
+extern "C" int mx_backend_debug_noalloc_scratch(const mx_backend* b, void** out) {
+  mx::clear_error();
+  if (!b || !out) return mx::set_error(MX_ERR_INVALID, "mx_backend_debug_noalloc_scratch: null argument");
+  *out = b->noalloc_scratch;
+  return MX_OK;
 }

@@ -63,6 +63,7 @@ typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
 constexpr int kSkMaxRows = 16;
 constexpr int kSkWaves = 8;
 constexpr int kSkLaneBytes = 8;  // bytes of one weight row per lane
+constexpr int kSkPlanCUs = 256;  // CUs the work split is planned for (MI355X)
 
 struct SkinnyArgs {
   const uint16_t* x;    // [M, K] bf16
@@ -577,7 +578,9 @@ int qdense_skinny_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   const bool i4 = dtype_is_packed(d.w_dt);
   const int64_t cols = i4 ? 256 : 128;
   const int64_t nb = (d.N + cols - 1) / cols;
-  const int ncu = b->num_cus > 0 ? b->num_cus : 256;
+  // The split (T, S, waves) fixes the summation order, so it is planned for MI355X's 256 CUs
+  // whatever the device reports: the same inputs give the same bits on every device.
+  const int ncu = kSkPlanCUs;
   const int waves = skinny_waves(d, nb, ncu);
   const int T = skinny_steps(d, nb, ncu, waves);
   const int64_t chunks = d.K / 32 / T;  // wave-sized pieces of one column block

@@ -152,9 +152,15 @@ typedef uint64_t mx_value;
  * config: comma-separated options: "device=N"; "host_only" (graph building and shape checks
  * only; every device operation then fails with MX_ERR_NO_DEVICE); "nofusion" (compile graphs op
  * by op); "exact" (FusedQuantizedDense always in the reference's loop order, bit-identical to
- * quantizeddense.go:586-650 at every size; without it, decode and prefill shapes take the fast
- * kernels, which differ only in summation order); "gemv_over_gemm" (measurement only: bf16 x with
- * 17..64 rows takes the GEMV even where the prefill GEMM fits, which it otherwise prefers). */
+ * quantizeddense.go:586-650 at every size).  Without "exact", decode and prefill shapes take the
+ * fast kernels.  The bf16-x kernels (skinny, prefill GEMM) and the decode GEMV differ from the
+ * reference only in summation order.  The prefill plans of the reference layout, f32 x, zero
+ * points and NF4 (past 64 rows), and of GGML rows (past 20 rows), also round each term's weight
+ * factor w*s (or w*s+zp) before the product with x, where the reference rounds (x*w)*s; they
+ * stay within the f32 accumulation bound of the reference's sum.  Problems of at most 2^24
+ * multiply-adds always take the reference-order kernel.  "gemv_over_gemm" (measurement only:
+ * bf16 x with 17..64 rows takes the GEMV even where the prefill GEMM fits, which it otherwise
+ * prefers). */
 int mx_backend_new(const char* config, mx_backend** out);
 /* Backend.Finalize (compute.go:95). Frees all device memory; later calls fail MX_ERR_FINALIZED. */
 int mx_backend_finalize(mx_backend* b);
@@ -187,6 +193,10 @@ int mx_backend_profile_reset(mx_backend* b);
 /* Host-side fault injection (no reference counterpart; failure-path tests): the n-th device
  * allocation from now fails with MX_ERR_OUT_OF_MEMORY (n <= 0 disables). */
 int mx_backend_debug_fail_alloc_after(mx_backend* b, int n);
+/* Inspection aid (no reference counterpart; tests): the device address of the static array that
+ * mx_qdense_noalloc uses on this backend's GPU (NULL for a host_only backend).  Backends on one
+ * GPU report the same address. */
+int mx_backend_debug_noalloc_scratch(const mx_backend* b, void** out);
 
 /* ---------------------------------------------------------------------------------------------
  * Buffers  —  compute.DataInterface (buffer.go:45-61) and compute.Buffer (buffer.go:12-43).
@@ -282,9 +292,19 @@ int mx_fn_dot_general(mx_function* fn, mx_value lhs, const int32_t* lhs_contract
                       const int32_t* rhs_contracting, int n_rc, const int32_t* rhs_batch, int n_rb,
                       int accumulator_dtype, int output_dtype, mx_value* out);
 
-/* FusedOps.FusedDense (fused_ops.go:347): weight layout [in, out...] only. */
+/* compute.DenseLayout (fused_ops.go:51-57). */
+enum { MX_DENSE_LAYOUT_INPUT_OUTPUTS = 0, MX_DENSE_LAYOUT_OUTPUTS_INPUT = 1 };
+/* compute.DenseConfig (fused_ops.go:73-77). */
+typedef struct mx_dense_config {
+  int32_t activation;    /* MX_ACT_*                                                          */
+  int32_t weight_layout; /* MX_DENSE_LAYOUT_*: weight [in, out...] or [out..., in]             */
+} mx_dense_config;
+/* FusedOps.FusedDense (fused_ops.go:347; reference builder fusedops/dense.go:34-110):
+ * y = act(x @ W + bias) for DenseLayoutInputOutputs, act(x @ W^T + bias) for
+ * DenseLayoutOutputsInput.  Output dims: x's leading dims, then the weight's output dims.
+ * options NULL = the zero DenseConfig (no activation, DenseLayoutInputOutputs). */
 int mx_fn_fused_dense(mx_function* fn, mx_value x, mx_value weight, mx_value bias,
-                      int activation, mx_value* out);
+                      const mx_dense_config* options, mx_value* out);
 /* FusedOps.FusedGelu (fused_ops.go:329). */
 int mx_fn_fused_gelu(mx_function* fn, mx_value x, int exact, mx_value* out);
 
@@ -378,9 +398,13 @@ int mx_qdense_plan(mx_backend* b, const mx_qdense_args* args, char* buf, size_t 
  * Results are bit-identical to mx_qdense's, except where mx_qdense would dequantise the weights
  * into an f32 copy (reference layout at prefill size): that problem runs the exact kernel, whose
  * result is bit-identical to the reference's; GGML rows there run the decode GEMV once per group
- * of four rows (within the f32 accumulation bound of the reference's sum). Every call on one GPU shares the array, from any
- * backend: calls that overlap on one GPU (several streams or backends) race. Launches are not
- * recorded in the backend's kernel profile. */
+ * of four rows (within the f32 accumulation bound of the reference's sum). Every call on one GPU
+ * shares the array, from any backend; the calls are ordered on the device (each call's stream
+ * waits for the previous call's completion event), so calls from several streams or backends run
+ * one after another.  Under graph capture that wait cannot be recorded: the caller must keep a
+ * captured call from overlapping any other mx_qdense_noalloc call on the GPU, or the shared
+ * arrival counters can be left wrong for every later call.  Launches are not recorded in the
+ * backend's kernel profile. */
 #define MX_QDENSE_NOALLOC_SCRATCH_BYTES (16u << 20)
 int mx_qdense_noalloc(mx_backend* b, const mx_qdense_args* args);
 

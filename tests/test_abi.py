@@ -216,6 +216,44 @@ def test_dot_general_shape_kat(host_backend):
     assert f.Shape(y2) == ca.Shape(ca.Float64, 5, 2, 4, 1)
 
 
+def test_fused_dense_layout_shapes(host_backend):
+    # fusedops/dense.go:59-80: InputOutputs contracts the weight's first axis, OutputsInput its last;
+    # the output is x's leading dims followed by the weight's output dims.
+    f = host_backend.Builder("dense").Main()
+    x = f.Parameter("x", ca.Shape(ca.Float32, 2, 5, 3))
+    w_io = f.Parameter("w_io", ca.Shape(ca.Float32, 3, 4, 6))
+    w_oi = f.Parameter("w_oi", ca.Shape(ca.Float32, 4, 6, 3))
+    b = f.Parameter("b", ca.Shape(ca.Float32, 4, 6))
+    y = f.FusedDense(x, w_io, b, ca.DenseConfig(ca.ActivationRelu))
+    assert f.Shape(y) == ca.Shape(ca.Float32, 2, 5, 4, 6)
+    y = f.FusedDense(x, w_oi, b, ca.DenseConfig(ca.ActivationGelu, ca.DenseLayoutOutputsInput))
+    assert f.Shape(y) == ca.Shape(ca.Float32, 2, 5, 4, 6)
+    y = f.FusedDense(x, w_oi, None, ca.DenseConfig(WeightLayout=ca.DenseLayoutOutputsInput))
+    assert f.Shape(y) == ca.Shape(ca.Float32, 2, 5, 4, 6)
+    assert f.Shape(f.FusedDense(x, w_io, None)) == ca.Shape(ca.Float32, 2, 5, 4, 6)
+
+
+@pytest.mark.parametrize("case", ["io_dim", "oi_dim", "layout", "rank"])
+def test_fused_dense_layout_errors(host_backend, case):
+    f = host_backend.Builder("dense").Main()
+    x = f.Parameter("x", ca.Shape(ca.Float32, 2, 3))
+    w = f.Parameter("w", ca.Shape(ca.Float32, 4, 3))  # [out, in]: wrong for InputOutputs
+    w1 = f.Parameter("w1", ca.Shape(ca.Float32, 3))
+    # The reference's messages (dense.go:52-53, 62-63, 71-72, 80).
+    want, call = {
+        "io_dim": (r"x's last dim \(3\) must match weight's first dim \(4\) for DenseLayoutInputOutputs",
+                   lambda: f.FusedDense(x, w, None, ca.DenseConfig())),
+        "oi_dim": (r"x's last dim \(3\) must match weight's last dim \(2\) for DenseLayoutOutputsInput",
+                   lambda: f.FusedDense(x, f.Parameter("w2", ca.Shape(ca.Float32, 3, 2)), None,
+                                        ca.DenseConfig(WeightLayout=ca.DenseLayoutOutputsInput))),
+        "layout": ("unknown WeightLayout", lambda: f.FusedDense(x, w, None, ca.DenseConfig(WeightLayout=7))),
+        "rank": (r"x must have rank >= 1 \(got 2\), weight must have rank >= 2 \(got 1\)",
+                 lambda: f.FusedDense(x, w1, None)),
+    }[case]
+    with pytest.raises(ca.ComputeError, match="FusedDense: " + want):
+        call()
+
+
 @pytest.mark.parametrize("case", ["dtype", "ncontract", "dim", "reuse", "range"])
 def test_dot_general_errors(host_backend, case):
     f = host_backend.Builder("e").Main()

@@ -3,8 +3,8 @@ BlockAxis = 1 (fused_ops.go:208-229), f32 or bf16 x, zero points (quantizeddense
 NF4 (quantizeddense.go:586-609), past the GEMV's 64 rows.  The weights are dequantised into f32
 the way the reference forms each term's weight factor and contracted on the f32 matrix cores, so
 only rounding order differs from the reference loop: every output must be within
-2^-22 |y| + 1e-5 * sum_k |term_k| of the exact (f64) value (and, for f32 x, bf16 outputs within
-half an ulp of bf16 on top).  Rows are sampled at the largest size (the oracle computes rows
+2^-22 |y| + 1e-5 * sum_k |term_k| of the exact (f64) value; with bf16 x the output is bf16, and
+the relative part of the bound is one bf16 ulp, 2^-8 |y|, instead.  Rows are sampled at the largest size (the oracle computes rows
 independently)."""
 import numpy as np
 import pytest

@@ -155,28 +155,65 @@ def test_random_batched(backend, dt, transposed):
         assert np.all(np.abs(got - truth) <= 1e-3 + 1e-2 * np.abs(truth))
 
 
+@pytest.mark.parametrize("layout", [ca.DenseLayoutInputOutputs, ca.DenseLayoutOutputsInput])
 @pytest.mark.parametrize("case", ["fused_dense_none", "fused_dense_relu"])
-def test_fused_dense_kats(backend, case):
+def test_fused_dense_kats(backend, case, layout):
+    # support/backendtest/fusedops.go:178-212; with DenseLayoutOutputsInput the same weights are
+    # given transposed ([out, in]) and the expected values are the same.
     k = GOLDEN[case]
     act = ca.ActivationNone if case.endswith("none") else ca.ActivationRelu
     x, w, b = (np.array(k[n], np.float32) for n in ("x", "w", "bias"))
+    if layout == ca.DenseLayoutOutputsInput:
+        w = np.ascontiguousarray(w.T)
     y, _ = run(backend, [(x, ca.Float32), (w, ca.Float32), (b, ca.Float32)],
-               lambda f, p: f.FusedDense(p[0], p[1], p[2], act))
+               lambda f, p: f.FusedDense(p[0], p[1], p[2], ca.DenseConfig(act, layout)))
     assert np.array_equal(y, np.array(k["want"], np.float32))
 
 
+@pytest.mark.parametrize("layout", [ca.DenseLayoutInputOutputs, ca.DenseLayoutOutputsInput])
 @pytest.mark.parametrize("act", range(6))
-def test_fused_dense_random(backend, act):
-    rng = np.random.default_rng(act)
+def test_fused_dense_random(backend, act, layout):
+    rng = np.random.default_rng(act + 10 * int(layout))
     x = rng.standard_normal((33, 100)).astype(np.float32)
     w = (rng.standard_normal((100, 50)) * 0.1).astype(np.float32)
     b = (rng.standard_normal(50) * 0.1).astype(np.float32)
-    y, _ = run(backend, [(x, ca.Float32), (w, ca.Float32), (b, ca.Float32)],
-               lambda f, p: f.FusedDense(p[0], p[1], p[2], ca.ActivationType(act)))
-    pre = x.astype(np.float64) @ w.astype(np.float64) + b
+    wg = w if layout == ca.DenseLayoutInputOutputs else np.ascontiguousarray(w.T)
+    y, _ = run(backend, [(x, ca.Float32), (wg, ca.Float32), (b, ca.Float32)],
+               lambda f, p: f.FusedDense(p[0], p[1], p[2], ca.DenseConfig(ca.ActivationType(act), layout)))
+    rc = 0 if layout == ca.DenseLayoutInputOutputs else 1
+    pre = O.dot_general(x.astype(np.float64), [1], [], wg.astype(np.float64), [rc], []) + b
     want = O.act(pre.astype(np.float32), act)
     scale = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64) + np.abs(b)
     assert np.all(np.abs(y - want) <= 1e-5 * scale + 1e-6)
+
+
+@pytest.mark.parametrize("dt", [ca.Float32, ca.BFloat16])
+@pytest.mark.parametrize("shape", [((2, 7, 64), (3, 5, 64)), ((300, 512), (1024, 512))])
+def test_fused_dense_outputs_input_shapes(backend, dt, shape):
+    """DenseLayoutOutputsInput with several output axes ([out..., in]) and at a matrix-core size:
+    output dims are x's leading dims then the weight's leading dims (dense.go:69-77)."""
+    xs, ws = shape
+    rng = np.random.default_rng(len(xs) + len(ws))
+    x = rng.standard_normal(xs).astype(np.float32)
+    w = (rng.standard_normal(ws) * 0.1).astype(np.float32)
+    b = (rng.standard_normal(ws[:-1]) * 0.1).astype(np.float32)
+    if dt == ca.BFloat16:
+        x, w, b = (O.bf16_to_f32(O.bf16_round(a)) for a in (x, w, b))
+        ins = [(O.bf16_round(a), dt) for a in (x, w, b)]
+    else:
+        ins = [(a, dt) for a in (x, w, b)]
+    y, odt = run(backend, ins, lambda f, p: f.FusedDense(p[0], p[1], p[2],
+                                                       ca.DenseConfig(ca.ActivationSilu, ca.DenseLayoutOutputsInput)))
+    assert odt == dt and y.shape == xs[:-1] + ws[:-1]
+    got = O.bf16_to_f32(y) if dt == ca.BFloat16 else y
+    pre = O.dot_general(x.astype(np.float64), [len(xs) - 1], [], w.astype(np.float64), [len(ws) - 1], []) + b
+    want = O.act(pre.astype(np.float32), ca.ActivationSilu)
+    if dt == ca.Float32:
+        scale = O.dot_general(np.abs(x).astype(np.float64), [len(xs) - 1], [], np.abs(w).astype(np.float64),
+                              [len(ws) - 1], []) + np.abs(b)
+        assert np.all(np.abs(got - want) <= 1e-5 * scale + 1e-6)
+    else:
+        assert np.all(np.abs(got - want) <= 1e-3 + 1e-2 * np.abs(want))
 
 
 # ---------------------------------------------------------------------------------------------

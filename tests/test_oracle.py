@@ -254,6 +254,63 @@ def test_qdense_nf4_one_hot_x():
     assert np.array_equal(y, table[p.w.astype(np.int64)])
 
 
+# Order of operations of the reference loop (quantizeddense.go:616-650): the output starts at the
+# bias, the terms are added in increasing k, and each term is ((x * w) * s), or x * (w * s + zp)
+# with zero points, (x * nf4[w]) * s for NF4, every operation rounded to f32.  Each case below has
+# an expected result that any other order or grouping changes.
+def _one_term(x_bits, w, s_bits, w_dtype=O.DT_INT8, zp_bits=None, scheme=O.QUANT_LINEAR):
+    p = _prob(1, 1, 1, w_dtype=w_dtype, block_axis=1, block_size=1, bias=False, zp=zp_bits is not None,
+              scheme=scheme)
+    p.x = np.array([[x_bits]], np.uint32).view(np.float32)
+    p.w = np.array([[w]], np.int8 if w_dtype == O.DT_INT8 else np.uint8)
+    p.scale = np.array([[s_bits]], np.uint32).view(np.float32)
+    if zp_bits is not None:
+        p.zp = np.array([[zp_bits]], np.uint32).view(np.float32)
+    return int(O.qdense_f32(p).view(np.uint32)[0, 0])
+
+
+def test_qdense_bias_is_added_first():
+    # bias 2^24, then eight terms of 1: each 2^24 + 1 rounds back to 2^24 (ties to even), so the
+    # result stays 2^24; summing the terms first would give 2^24 + 8.
+    K = 8
+    p = _prob(1, K, 1, w_dtype=O.DT_INT8, block_axis=1, block_size=1, bias=True)
+    p.x = np.ones((1, K), np.float32)
+    p.w = np.ones((K, 1), np.int8)
+    p.scale = np.ones((K, 1), np.float32)
+    p.bias = np.array([2.0 ** 24], np.float32)
+    assert O.qdense_f32(p)[0, 0] == np.float32(2.0 ** 24)
+
+
+def test_qdense_terms_in_increasing_k():
+    # x = [2^24, 1 (six times), -2^24]: in increasing k the six ones are lost against 2^24 and the
+    # result is 0; decreasing k gives 6, and pairwise or blocked sums give other values.
+    K = 8
+    p = _prob(1, K, 1, w_dtype=O.DT_INT8, block_axis=1, block_size=1, bias=False)
+    p.x = np.array([[2.0 ** 24] + [1.0] * 6 + [-(2.0 ** 24)]], np.float32)
+    p.w = np.ones((K, 1), np.int8)
+    p.scale = np.ones((K, 1), np.float32)
+    assert O.qdense_f32(p)[0, 0] == np.float32(0.0)
+
+
+def test_qdense_term_is_x_times_w_then_scale():
+    # x = -0.96694475 (bits 3212282289), w = -59, s = 0.008319432 (bits 1007177274):
+    # (x * w) * s rounds to bits 1056113044; x * (w * s) would round to 1056113045.
+    assert _one_term(3212282289, -59, 1007177274) == 1056113044
+
+
+def test_qdense_zero_point_term_grouping():
+    # x * (w * s + zp) with x bits 1063174608, w = 27, s bits 1007202239, zp bits 3175853478 rounds
+    # to bits 1042048540; (x * w) * s + x * zp gives 1042048542 and x * (w * s) + x * zp gives
+    # 1042048541.
+    assert _one_term(1063174608, 27, 1007202239, zp_bits=3175853478) == 1042048540
+
+
+def test_qdense_nf4_term_is_x_times_value_then_scale():
+    # NF4 code 12, x bits 1019326333, s bits 991334551: (x * nf4[12]) * s rounds to bits 935907406;
+    # x * (nf4[12] * s) would round to 935907407.
+    assert _one_term(1019326333, 12, 991334551, w_dtype=O.DT_UINT8, scheme=O.QUANT_NF4) == 935907406
+
+
 def test_qdense_threads_do_not_change_result():
     p = O.make_problem(1, 256, 300, w_dtype=O.DT_INT4, block_axis=0, block_size=64, seed=3)
     assert np.array_equal(O.qdense_f32(p, threads=1), O.qdense_f32(p, threads=4))

@@ -139,15 +139,47 @@ def test_noalloc_rejects_oversized_scratch(backend):
     assert np.array_equal(got, ref)
 
 
-def test_noalloc_second_backend_shares_array():
+def test_noalloc_second_backend_shares_array(backend):
     """A second backend on the same GPU gets the same static array (set up once per device) and
     computes the same result."""
     b2 = ca.New("mi355x")
     try:
+        assert backend.DebugNoAllocScratch() != 0
+        assert b2.DebugNoAllocScratch() == backend.DebugNoAllocScratch()
         d = Direct(b2, SKINNY[0])
         ref, got = d.run_both()
         assert np.array_equal(got, ref)
         assert_bf16_close(got, O.qdense_f32(SKINNY[0], threads=8), what="second backend")
+    finally:
+        b2.Finalize()
+
+
+def test_noalloc_calls_from_two_streams_are_ordered(backend):
+    """Calls queued back to back on two backends' streams (no host synchronisation between them),
+    alternating problems whose split-K slice counts and column blocks differ, each give
+    mx_qdense's bits: every call's stream waits for the previous call on the GPU, so no two calls
+    share the static array at once and the arrival counters stay consistent."""
+    b2 = ca.New("mi355x")
+    try:
+        cases = [Direct(backend, SKINNY[0]), Direct(b2, SKINNY_I8[0]), Direct(b2, GEMV[0]),
+                 Direct(backend, SKINNY[1])]
+        refs = []
+        for d in cases:
+            assert d.call("mx_qdense", d.outs[0]) == _lib.MX_OK
+            refs.append(d.outs[0].ToFlatData().reshape(d.p.M, d.p.N))
+        outs = []
+        for rnd in range(3):
+            for d in cases:
+                sh = ca.Shape(DT[d.p.x_dtype], d.p.M, d.p.N)
+                o = d.backend.BufferFromFlatData(0, np.zeros(d.p.M * d.p.N, sh.dtype.numpy_storage()), sh)
+                d.backend.Synchronize()  # the upload is done before any call is queued
+                outs.append((d, o))
+        for d, o in outs:
+            rc = d.call("mx_qdense_noalloc", o)
+            assert rc == _lib.MX_OK, d.backend._lib.mx_last_error().decode()
+        for i, (d, o) in enumerate(outs):
+            got = o.ToFlatData().reshape(d.p.M, d.p.N)
+            assert np.array_equal(got, refs[i % len(cases)]), f"call {i} ({d.p.M}x{d.p.K}x{d.p.N}) differs"
     finally:
         b2.Finalize()
 
