@@ -25,7 +25,7 @@ COMMON = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-SOURCES = ["runtime.cpp", "graph.cpp", "qdense.hip", "qdense_skinny.hip", "qdense_gemv.hip", "qdense_gemm.hip", "qdense_noalloc.hip", "ggml.hip", "dot.hip", "elementwise.hip"]
+SOURCES = ["runtime.cpp", "graph.cpp", "qdense.hip", "qdense_skinny.hip", "qdense_gemv.hip", "qdense_gemm.hip", "qdense_refgemm.hip", "qdense_noalloc.hip", "ggml.hip", "dot.hip", "elementwise.hip"]
 
 
 # The skinny kernel takes one arrival ticket per workgroup from a single lane; LLVM's atomic

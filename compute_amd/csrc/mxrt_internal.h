@@ -270,6 +270,11 @@ const char* ggml_plan_name(const mx_backend* b, const GgmlDesc& d);
 int ggml_dense_run(mx_backend* b, const GgmlDesc& d);
 int ggml_embed_run(mx_backend* b, const GgmlEmbedDesc& e);
 
+// Prefill of the reference layout, f32 x, zero points and NF4 (qdense_refgemm.hip): the weights
+// dequantised per K block into LDS, the contraction on the f32 matrix cores.
+bool qdense_refgemm_fits(const QDenseDesc& d);
+int qdense_refgemm_run(mx_backend* b, const QDenseDesc& d, const char* name);
+
 // Prefill MFMA GEMM (qdense_gemm.hip): shape/layout check and launch.
 bool qdense_gemm_fits(const QDenseDesc& d);
 int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name);

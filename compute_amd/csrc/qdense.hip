@@ -13,8 +13,13 @@
 // Kernels (selected in this order):
 //   qdense_skinny_mfma (qdense_skinny.hip) — M <= 16 bf16 rows (decode, small batches), scales
 //                    blocked along K: HBM-bound streaming of the weights into MFMA operands.
-//   qdense_gemm_mfma (qdense_gemm.hip) — M > 16 bf16 rows, int8/uint8 weights, one scale per
-//                    output column (prefill): bf16 MFMA GEMM with on-the-fly dequantisation.
+//   qdense_gemm_mfma (qdense_gemm.hip) — M > 16 bf16 rows, int8/uint8/int4/uint4 weights, one
+//                    scale per output column or per group of 64k rows (prefill): bf16 MFMA GEMM
+//                    with on-the-fly dequantisation.
+//   qdense_gemv (qdense_gemv.hip) — up to 64 rows of the reference's own layout, f32 x, zero
+//                    points, NF4: HBM-bound decode GEMV.
+//   qdense_refgemm_f32_mfma (qdense_refgemm.hip) — the same variants past the GEMV: f32 MFMA
+//                    GEMM with each K block of weights dequantised into LDS.
 //   qdense_exact   — one output column per thread, k in order, each term rounded exactly as the
 //                    reference loop rounds it: bit-identical to the reference's f32 result.
 //                    Used for f32 activations and every shape/layout without a fast path.
@@ -352,90 +357,21 @@ static int exact_rows(const QDenseDesc& d) {
 
 // =============================================================================================
 // Reference layout and variants at prefill size (scale [K, ceil(N/B)] with BlockAxis = 1, f32 x,
-// zero points, NF4): the weights are dequantised once into f32 as the reference forms each
-// term's weight factor (w*s, or w*s + zp, quantizeddense.go:586-650), the contraction runs on the
-// f32 matrix cores (dot_run), and the epilogue adds the bias and applies the reference
-// activation.  Per term this is x*(w*s) where the reference rounds (x*w)*s (zero points: the
-// same x*(w*s + zp)); with the f32 sums in another order, the result stays within the f32
-// accumulation bound of the reference's.
+// zero points, NF4): the fused dequantise-and-contract kernel of qdense_refgemm.hip (f32 matrix
+// cores, the weights dequantised per K block into LDS).  Problems of at most 2^24 multiply-adds
+// keep the exact kernel (the reference's own BenchmarkQuantizedDense shapes, up to
+// 32 x 512 x 1024, stay bit-identical to it).
 // =============================================================================================
-// Problems of at most 2^24 multiply-adds keep the exact kernel (the reference's own
-// BenchmarkQuantizedDense shapes, up to 32 x 512 x 1024, stay bit-identical to it).
-constexpr int64_t kDeqMinMKN = (int64_t)1 << 24;
-constexpr int64_t kDeqMaxWeightBytes = (int64_t)8 << 30;  // f32 copy of the weights
+constexpr int64_t kRefGemmMinMKN = (int64_t)1 << 24;
 
-__global__ void qdense_dequant_f32_kernel(QDenseDesc d, float* __restrict__ wf) {
-  const int64_t N = d.N, B = d.block_size, total = d.K * d.N;
-  const int64_t nb = (N + B - 1) / B;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t k = i / N, n = i - k * N;
-    const int wi = decode_weight(d.w, i, d.w_dt);
-    const int64_t si = d.block_axis == 1 ? k * nb + n / B : (k / B) * N + n;
-    const float s = load_f(d.scale, si, d.s_dt);
-    const float w = d.scheme == MX_QUANT_NF4 ? kNF4Table[(uint32_t)wi & 15u] : (float)wi;
-    wf[i] = d.zp ? add_rn(mul_rn(w, s), load_f(d.zp, si, d.zp_dt)) : mul_rn(w, s);
-  }
-}
-
-__global__ void qdense_epilogue_kernel(const float* __restrict__ acc, const void* bias, int b_dt, void* out, int out_dt,
-                                       int act, int64_t M, int64_t N) {
-  const int64_t total = M * N;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t n = i % N;
-    const float v = bias ? add_rn(load_f(bias, n, b_dt), acc[i]) : acc[i];
-    store_f(out, i, out_dt, act_ref(v, act));
-  }
-}
-
-static bool qdense_dequant_fits(const QDenseDesc& d) {
-  auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
-  return (d.scheme == MX_QUANT_LINEAR || d.scheme == MX_QUANT_NF4) &&
-         (d.x_dt == MX_DTYPE_FLOAT32 || d.x_dt == MX_DTYPE_BFLOAT16) && d.M > 4 && d.K % 4 == 0 &&
-         d.M * d.K * d.N > kDeqMinMKN && d.K * d.N * 4 <= kDeqMaxWeightBytes && d.M < (1 << 24) &&
-         d.K < (1 << 24) && d.N < (1 << 24) && aligned(d.x, 16);
-}
-
-static int qdense_dequant_run(mx_backend* b, const QDenseDesc& d, const char* name) {
-  hipStream_t st = b->stream;
-  void *wf = nullptr, *xf = nullptr, *acc = nullptr;
-  auto release = [&] {
-    if (wf) dev_free(b, wf);
-    if (xf) dev_free(b, xf);
-    if (acc) dev_free(b, acc);
-  };
-  int rc = dev_alloc(b, (size_t)(d.K * d.N) * 4, &wf);
-  if (rc == MX_OK && d.x_dt != MX_DTYPE_FLOAT32) rc = dev_alloc(b, (size_t)(d.M * d.K) * 4, &xf);
-  if (rc == MX_OK) rc = dev_alloc(b, (size_t)(d.M * d.N) * 4, &acc);
-  if (rc == MX_OK)
-    rc = launch(b, name, [&] { dispatch(qdense_dequant_f32_kernel, 2048, 256, 0, st, d, (float*)wf); });
-  if (rc == MX_OK && xf) rc = ew_convert(b, d.x, d.x_dt, xf, MX_DTYPE_FLOAT32, d.M * d.K);
-  if (rc == MX_OK) {
-    DotDesc dd{};
-    dd.lhs = xf ? xf : d.x;
-    dd.rhs = wf;
-    dd.out = acc;
-    dd.B = 1;
-    dd.M = d.M;
-    dd.K = d.K;
-    dd.N = d.N;
-    dd.rhs_transposed = false;
-    dd.in_dt = MX_DTYPE_FLOAT32;
-    dd.out_dt = MX_DTYPE_FLOAT32;
-    rc = dot_run(b, dd);
-  }
-  if (rc == MX_OK)
-    rc = launch(b, "qdense_epilogue", [&] {
-      dispatch(qdense_epilogue_kernel, 1024, 256, 0, st, (const float*)acc, d.bias, d.b_dt, d.out, d.x_dt, d.act, d.M,
-               d.N);
-    });
-  release();  // stream-ordered pool: later users run after these kernels
-  return rc;
+static bool qdense_refgemm_plan(const QDenseDesc& d) {
+  return d.M > 4 && d.M * d.K * d.N > kRefGemmMinMKN && qdense_refgemm_fits(d);
 }
 
 // =============================================================================================
 // Kernel selection.
 // =============================================================================================
-enum class QPath { kEmpty, kExact, kSkinny, kSkinnyRows, kGemv, kGemm, kDequant };
+enum class QPath { kEmpty, kExact, kSkinny, kSkinnyRows, kGemv, kGemm, kRefGemm };
 
 // Past 16 rows of bf16 x: the skinny kernel once per group of 16 rows (its row limit).  Each
 // launch streams the weights once at decode rate (13-17 us per 16 rows at [4096] x 11008-14336
@@ -478,16 +414,15 @@ static QPath choose_path(const mx_backend* b, const QDenseDesc& d) {
   if (!b->gemv_over_gemm && qdense_gemm_fits(d)) return QPath::kGemm;
   if (qdense_gemv_fits(d)) return QPath::kGemv;
   if (qdense_gemm_fits(d)) return QPath::kGemm;
-  // The dequantised f32 copy of the weights is a device allocation: without one the exact
-  // kernel runs (allocation-free, bit-identical to the reference).
-  if (!b->noalloc_active && qdense_dequant_fits(d)) return QPath::kDequant;
+  // The reference layout, f32 x, zero points and NF4 at prefill size: the fused kernel.
+  if (qdense_refgemm_plan(d)) return QPath::kRefGemm;
   return QPath::kExact;
 }
 
 static const char* path_name(const QDenseDesc& d, QPath p) {
   switch (p) {
     case QPath::kEmpty: return "empty";
-    case QPath::kDequant: return "qdense_dequant_f32_mfma";
+    case QPath::kRefGemm: return "qdense_refgemm_f32_mfma";
     case QPath::kGemm:
       switch (d.w_dt) {
         case MX_DTYPE_INT8: return d.block_size < d.K ? "qdense_gemm_mfma_i8_grouped" : "qdense_gemm_mfma_i8";
@@ -602,8 +537,8 @@ int qdense_run(mx_backend* b, const QDenseDesc& d) {
       return qdense_gemv_run(b, d, name);
     case QPath::kGemm:
       return qdense_gemm_run(b, d, name);
-    case QPath::kDequant:
-      return qdense_dequant_run(b, d, name);
+    case QPath::kRefGemm:
+      return qdense_refgemm_run(b, d, name);
     default: {
       const int R = exact_rows(d);
       dim3 grid((unsigned)((d.N + kExactThreads - 1) / kExactThreads), (unsigned)((d.M + R - 1) / R));

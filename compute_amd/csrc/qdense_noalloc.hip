@@ -7,8 +7,8 @@
 //     `scratch`, a static device array of MX_QDENSE_NOALLOC_SCRATCH_BYTES that every GPU the
 //     library runs on holds until the process ends, instead of the backend's growable scratch;
 //     a problem that needs more is rejected before anything is launched;
-//   - a problem that mx_qdense would compute through a dequantised f32 copy of the weights runs
-//     the exact kernel, which needs no workspace;
+//   - GGML rows past 20 rows, which mx_qdense dequantises into an f32 copy for the f32 matrix
+//     cores, run the decode GEMV once per group of four rows instead;
 //   - any other device allocation reached during the call is an error (dev_alloc refuses it).
 //
 // Layout of `scratch` (the same as the backend's scratch): bytes [0, 64 KiB) are the arrival

@@ -41,7 +41,8 @@ class QDenseRun:
         self.exe = bld.Compile()
         self.inputs = [backend.BufferFromFlatData(0, d.ravel(), sh) for d, sh in zip(datas, shapes)]
 
-    def plan(self) -> str:
+    def args(self, out=None):
+        """mx_qdense_args over the resident inputs; out: the output buffer (planning: none)."""
         p = self.p
         a = ca._lib.mx_qdense_args()
         a.x, a.w, a.scale = (self.inputs[i].DevicePtr() for i in range(3))
@@ -53,11 +54,18 @@ class QDenseRun:
         if p.bias is not None:
             a.bias = self.inputs[k].DevicePtr()
             a.bias_dtype = p.bias_dtype
-        a.out = self.inputs[0].DevicePtr()  # not written by planning
+        a.out = (out or self.inputs[0]).DevicePtr()  # planning writes nothing
         a.M, a.K, a.N = p.M, p.K, p.N
         a.x_dtype, a.w_dtype, a.scale_dtype = p.x_dtype, p.w_dtype, p.scale_dtype
         a.scheme, a.block_axis, a.block_size, a.activation = p.scheme, p.block_axis, p.block_size, p.act
-        return self.backend.QDensePlan(a)
+        return a
+
+    def plan(self) -> str:
+        return self.backend.QDensePlan(self.args())
+
+    def run_direct(self, out) -> None:
+        """mx_qdense on the resident inputs into the caller's output buffer (no graph)."""
+        self.backend.QDense(self.args(out))
 
     def run(self) -> np.ndarray:
         out = self.exe.Execute(self.inputs)[0]

@@ -369,7 +369,7 @@ def test_qdense_plan_selection():
                          block_size=64) == want("qdense_gemm_mfma_i8_grouped")
             # Groups that do not tile K in 64-row blocks take the f32 dequantise-and-contract path.
             assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
-                         block_size=96) == want("qdense_dequant_f32_mfma")
+                         block_size=96) == want("qdense_refgemm_f32_mfma")
             # Small problems, M > 64 with the reference layout, unsupported block sizes: reference order.
             assert _plan(b, 1, 512, 1024, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=64) == "qdense_exact"
@@ -377,9 +377,9 @@ def test_qdense_plan_selection():
                          block_size=64) == want("qdense_gemv_i8")
             # Past the GEMV's 64 rows, the reference layout dequantises into f32 for the matrix cores.
             assert _plan(b, 65, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
-                         block_size=64) == want("qdense_dequant_f32_mfma")
+                         block_size=64) == want("qdense_refgemm_f32_mfma")
             assert _plan(b, 512, 4096, 4096, x_dtype=BF16, w_dtype=ca.Uint4, s_dtype=F32, block_axis=1,
-                         block_size=128, scheme=1) == want("qdense_dequant_f32_mfma")
+                         block_size=128, scheme=1) == want("qdense_refgemm_f32_mfma")
             assert _plan(b, 1, 4096, 4096, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=16) == "qdense_exact"
             # The reference's BenchmarkQuantizedDense shapes (at most 2^24 multiply-adds) keep the
@@ -388,7 +388,7 @@ def test_qdense_plan_selection():
                 assert _plan(b, 32, 512, 1024, x_dtype=F32, w_dtype=w_dt, s_dtype=F32, block_axis=1,
                              block_size=128, scheme=scheme) == "qdense_exact"
                 assert _plan(b, 33, 512, 1024, x_dtype=F32, w_dtype=w_dt, s_dtype=F32, block_axis=1,
-                             block_size=128, scheme=scheme) == want("qdense_dequant_f32_mfma")
+                             block_size=128, scheme=scheme) == want("qdense_refgemm_f32_mfma")
         finally:
             b.Finalize()
     b = ca.New("host_only,gemv_over_gemm")

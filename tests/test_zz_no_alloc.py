@@ -2,13 +2,11 @@
 mx_qdense on the same device buffers.
 
 The allocation-free entry point runs mx_qdense's kernels with their split-K scratch taken from a
-static per-GPU array, so on the skinny, GEMV and GEMM paths its result must be bit-identical to
-mx_qdense's, and within the oracle bars of those paths (bf16 outputs rel 1e-2 / abs 1e-3 of the
-reference's f32 result).  Where mx_qdense dequantises the weights into an f32 copy, the
-allocation-free call runs the exact kernel: its result must equal the oracle's restatement of the
-reference loop bit for bit, and mx_qdense's within the f32 accumulation bound.  GGML rows past 20
-rows, which mx_qdense also dequantises, take the GEMV once per group of four rows on the
-allocation-free call, within the same bound.  Each case makes two
+static per-GPU array, so on the skinny, GEMV, GEMM and fused reference-layout paths its result
+must be bit-identical to mx_qdense's, and within the oracle bars of those paths (bf16 outputs rel
+1e-2 / abs 1e-3 of the reference's f32 result, f32 outputs the f32 accumulation bound).  GGML rows
+past 20 rows, which mx_qdense dequantises into an f32 copy, take the GEMV once per group of four
+rows on the allocation-free call, within the same bound.  Each case makes two
 calls in a row, the second on a smaller problem, as a caller reusing the shared array would.
 """
 import ctypes as C
@@ -106,19 +104,18 @@ def test_noalloc_matches_qdense(backend, pair, plan):
             assert_f32_accumulation_close(got, p, what=f"{p.M}x{p.K}x{p.N}")
 
 
-def test_noalloc_reference_layout_runs_exact(backend):
-    """Reference layout at prefill size: mx_qdense dequantises into an f32 weight copy, the
-    allocation-free call runs the exact kernel (the reference's loop order)."""
+def test_noalloc_reference_layout_fused(backend):
+    """Reference layout at prefill size: both entry points run the fused kernel, which dequantises
+    each K block into LDS and needs no workspace, so the results are bit-identical."""
     pair = [problem(96, 512, 1024, 9, w_dtype=O.DT_INT4, x_dtype=O.DT_FLOAT32, block_axis=1, block_size=64),
             problem(64, 512, 768, 10, w_dtype=O.DT_UINT8, x_dtype=O.DT_FLOAT32, block_axis=1, block_size=32,
                     zp=True)]
     for p in pair:
         d = Direct(backend, p)
-        assert backend.QDensePlan(d.args(d.outs[0])) == "qdense_dequant_f32_mfma"
+        assert backend.QDensePlan(d.args(d.outs[0])) == "qdense_refgemm_f32_mfma"
         ref, got = d.run_both()
-        want = O.qdense_f32(p, threads=8)
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "exact path differs from the reference loop"
-        assert_f32_accumulation_close(ref, p, what="mx_qdense (dequantised f32 weights)")
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "mx_qdense_noalloc differs from mx_qdense"
+        assert_f32_accumulation_close(got, p, what="fused reference layout")
 
 
 def test_noalloc_rejects_oversized_scratch(backend):
