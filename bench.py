@@ -15,10 +15,11 @@ R1, the reference's own layout at the C2 shape (f32 x, Int4, scales [4096, 86]; 
 and D1, bf16 DotGeneral at the C4 shape (bf16 MFMA roofline).
 
 `value` is algorithmic bytes per step / wall time per step over K back-to-back steps (host
-launch overhead included).  `roofline` prices the dominant kernel's average duration, taken from
-HIP events recorded on the backend's stream around every launch over K more steps; where one
-kernel is the whole step and those events read longer than the unperturbed wall time per step
-(long prefill kernels), the wall time per step is used instead (`kernel_us_source` says which).
+launch overhead included).  `roofline` prices the dominant kernel's average duration: where one
+kernel is the whole step, the device time per step of the same timed region (a HIP event pair on
+the backend's stream around the K launches); otherwise HIP events recorded around every launch
+over K more steps (`kernel_us_source` says which; per-launch events add work between kernels and
+read longer, so they are used only to split a multi-kernel step).
 Weight sets are handed out in one rotation across the warm-up, timed and event-timed loops, so
 no loop starts on a set that is still in the Infinity Cache.
 `traffic` (HBM bytes per launch) is read from profiles/traffic.json, which is produced from
@@ -66,8 +67,9 @@ def measure(backend, wl, steps: int, warmup: int, rotate_bytes: int = 2 * MALL_B
     HIP event pair around every kernel launch (per-kernel average durations)."""
     exe = wl.compile(backend)
     n_sets = max(1, math.ceil(rotate_bytes / max(1, wl.weight_bytes())))
+    capped = n_sets > 64  # tiny weights (C1): 64 sets still fit the cache; such a case is latency-bound
     n_sets = min(n_sets, 64)
-    if rotate_bytes:
+    if rotate_bytes and not capped:
         # A set is read again only after the other n_sets - 1 sets: more than the MALL apart.
         assert (n_sets - 1) * wl.weight_bytes() > MALL_BYTES, (wl.name, n_sets)
     rot = Rotation([wl.upload(backend) for _ in range(n_sets)])
@@ -76,8 +78,9 @@ def measure(backend, wl, steps: int, warmup: int, rotate_bytes: int = 2 * MALL_B
     backend.Synchronize()
     timed = rot.take(steps)
     t0 = time.perf_counter()
+    backend.RegionBegin()
     exe.ExecuteLoop(timed, steps)
-    backend.Synchronize()
+    region_ms = backend.RegionEnd()  # waits for the stream: the timed region ends here
     wall = time.perf_counter() - t0
     backend.SetProfiling(True)
     backend.ProfileReset()
@@ -92,17 +95,19 @@ def measure(backend, wl, steps: int, warmup: int, rotate_bytes: int = 2 * MALL_B
     kernels = {k: {"launches_per_step": v[0] / steps, "avg_us": v[1] / v[0] * 1e3} for k, v in prof.items()}
     kname = max(prof.items(), key=lambda kv: kv[1][1])[0]
     kernel_us_per_step = sum(v[1] for v in prof.values()) / steps * 1e3
-    wall_us = wall / steps * 1e3 * 1e3
-    kernel_us = kernels[kname]["avg_us"]
-    source = "hip_events"
-    if len(prof) == 1 and kernels[kname]["launches_per_step"] == 1 and kernel_us > wall_us:
-        # One kernel per step, run back to back: its duration cannot exceed the wall time per
-        # step.  The per-launch events then slowed the kernels they timed (long prefill
-        # kernels), and the unperturbed wall time per step is the (conservative) duration.
-        kernel_us, source = wall_us, "wall_per_step (per-launch events read %.3f us)" % kernels[kname]["avg_us"]
+    region_us = region_ms / steps * 1e3
+    if len(prof) == 1 and kernels[kname]["launches_per_step"] == 1:
+        # One kernel per step: its average duration is the device time of the timed region per
+        # step (an event pair on the backend's stream around the back-to-back launches; the
+        # inter-dispatch gap is included, so this errs low on the achieved rate).  Per-launch
+        # events add work between the kernels and read longer.
+        kernel_us, source = region_us, "hip_events_region (per-launch events read %.3f us)" % kernels[kname]["avg_us"]
+        kernel_us_per_step = region_us
+    else:
+        kernel_us, source = kernels[kname]["avg_us"], "hip_events_per_launch"
     return {"ms_per_step": wall / steps * 1e3, "kernel": kname, "kernel_us": kernel_us, "kernel_us_source": source,
-            "kernels": kernels, "kernel_us_per_step": min(kernel_us_per_step, wall_us) if len(prof) == 1 else
-            kernel_us_per_step, "weight_sets": n_sets}
+            "kernels": kernels, "kernel_us_per_step": kernel_us_per_step, "region_us_per_step": region_us,
+            "weight_sets": n_sets}
 
 
 def traffic_for(name: str):
@@ -234,7 +239,8 @@ def copy_calibration(mib: int, iters: int):
 def extra_entry(wl, r):
     nbytes = wl.algorithmic_bytes()
     e = {"us_per_call": round(r["ms_per_step"] * 1e3, 2), "kernel": r["kernel"], "kernel_us": round(r["kernel_us"], 3),
-         "kernel_us_source": r["kernel_us_source"], "kernel_us_per_call": round(r["kernel_us_per_step"], 3)}
+         "kernel_us_source": r["kernel_us_source"], "kernel_us_per_call": round(r["kernel_us_per_step"], 3),
+         "device_us_per_call": round(r["region_us_per_step"], 3)}
     if wl.name.startswith("C4") or wl.name.startswith("D1") or wl.name.startswith("Q"):
         e["TFLOPs_kernel"] = round(wl.flops() / (r["kernel_us"] * 1e-6) / 1e12, 1)
         e["roofline"] = mfma_roofline(wl.flops(), r["kernel_us"], traffic_for(wl.name))
@@ -246,12 +252,12 @@ def extra_entry(wl, r):
                         for k, v in r["kernels"].items()}
         e["roofline"] = mfma_roofline(wl.flops(), r["kernel_us_per_step"], traffic_for(wl.name), F32_PEAK_TFLOPS)
     elif wl.name.startswith("C5"):
-        # Whole graph per call: the three quantized projections dominate; price all kernels of one
-        # call against HBM.
+        # Whole graph per call: the three quantized projections dominate; price one call's device
+        # time (the timed region per call, all kernels and the gaps between them) against HBM.
         e["GBps_call"] = round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1)
         e["kernels"] = {k: {"per_call": round(v["launches_per_step"], 2), "avg_us": round(v["avg_us"], 3)}
                         for k, v in r["kernels"].items()}
-        e["roofline"] = hbm_roofline(nbytes, r["kernel_us_per_step"], traffic_for(wl.name))
+        e["roofline"] = hbm_roofline(nbytes, r["region_us_per_step"], traffic_for(wl.name))
     else:
         e["GBps_kernel"] = round(nbytes / (r["kernel_us"] * 1e-6) / 1e9, 1)
         e["roofline"] = hbm_roofline(nbytes, r["kernel_us"], traffic_for(wl.name))

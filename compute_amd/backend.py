@@ -372,6 +372,16 @@ class Backend:
     def DebugFailAllocAfter(self, n: int) -> None:
         _check(self._lib.mx_backend_debug_fail_alloc_after(self._h, n))
 
+    def RegionBegin(self) -> None:
+        """Records the start event of a timed stretch of queued work on the backend's stream."""
+        _check(self._lib.mx_backend_region_begin(self._h))
+
+    def RegionEnd(self) -> float:
+        """Records the end event, waits for it; returns the device milliseconds since RegionBegin."""
+        ms = C.c_double()
+        _check(self._lib.mx_backend_region_end(self._h, C.byref(ms)))
+        return ms.value
+
     def DebugNoAllocScratch(self) -> int:
         """Device address of the static array mx_qdense_noalloc uses on this backend's GPU."""
         p = C.c_void_p()

@@ -141,6 +141,9 @@ struct mx_backend {
   std::vector<mx::PendingTiming> pending;
   std::vector<hipEvent_t> event_cache;
   std::map<std::string, mx::ProfEntry> prof;
+  // mx_backend_region_begin / _end: one event pair around a stretch of queued work.
+  hipEvent_t region_start = nullptr, region_stop = nullptr;
+  bool region_open = false;
 
   int64_t live_buffers = 0;
 };

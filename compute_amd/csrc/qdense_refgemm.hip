@@ -65,10 +65,17 @@ __device__ __forceinline__ float rg_load(const void* p, int64_t i, int dt) {
   return dt == MX_DTYPE_BFLOAT16 ? bf16_to_f32(((const uint16_t*)p)[i]) : ((const float*)p)[i];
 }
 
-template <int WDT, int SM>
+// PLAIN: f32 x, linear scheme, no zero points: the common case, with every dtype test of the
+// general kernel resolved at compile time.
+template <int WDT, int SM, bool PLAIN>
 __global__ __launch_bounds__(kRgThreads, 2) void qdense_refgemm_kernel(RefGemmArgs a) {
   constexpr bool kI4 = WDT == MX_DTYPE_INT4 || WDT == MX_DTYPE_UINT4;
   constexpr bool kSigned = WDT == MX_DTYPE_INT4 || WDT == MX_DTYPE_INT8;
+  if constexpr (PLAIN) {
+    a.x_dt = MX_DTYPE_FLOAT32;
+    a.zp = nullptr;
+    a.nf4 = 0;
+  }
   __shared__ __attribute__((aligned(16))) char sm[2][kRgBuf];
   __shared__ float nf4[16];
 
@@ -94,23 +101,32 @@ __global__ __launch_bounds__(kRgThreads, 2) void qdense_refgemm_kernel(RefGemmAr
   const int blo = SM == kRgCols ? 0 : ncl / a.B;
   const int jsplit = SM == kRgBlk ? min(16, (blo + 1) * a.B - ncl) : 16;
 
+  // Every load below is unconditional (dtype choices only select addresses or bits), so that the
+  // compiler waits for a block's loads where they are used, not where they are issued.
+  const bool sbf = a.s_dt == MX_DTYPE_BFLOAT16, zbf = a.zp_dt == MX_DTYPE_BFLOAT16;
   struct Regs {
     u32x4_v x[4];
-    u32x4_v w;      // 16 bytes (int8) or 8 (Int4, in .xy)
-    uint32_t s[16]; // raw scale words (kRgCols f32: 16; bf16: 8 holding pairs; kRgBlk: 2)
-    uint32_t z[16];
+    u32x4_v w;       // 16 bytes (int8) or 8 (Int4, in .xy)
+    uint32_t s[16];  // raw scale words (kRgCols: 16 f32 or 8 bf16 pairs; kRgBlk: 2; kRgAny: 16)
+    uint32_t z[16];  // the same for zero points
+    uint32_t ssh[16], zsh[16];  // kRgBlk / kRgAny: shift moving a bf16 element to the high half
+  };
+  // The aligned word holding element i of an f32 or bf16 array, and its shift.
+  auto word = [&](const void* p, int64_t i, bool bf, uint32_t& w, uint32_t& sh) __attribute__((always_inline)) {
+    const uintptr_t ad = (uintptr_t)p + (uintptr_t)i * (bf ? 2 : 4);
+    w = *(const uint32_t*)(ad & ~(uintptr_t)3);
+    sh = bf && (ad & 2) == 0 ? 16u : 0u;
   };
   auto gload = [&](int kb, Regs& R) __attribute__((always_inline)) {
     const int k0 = kb * kRgBK;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      if (!xbf || p < 2) {
-        const int c = t + 256 * p;
-        const int row = xbf ? c >> 2 : c >> 3, kc = xbf ? (c & 3) * 8 : (c & 7) * 4;
-        const int m = min(m0 + row, M - 1);
-        const int k = min(k0 + kc, K - (xbf ? 8 : 4));
-        R.x[p] = *(const u32x4_v*)((const char*)a.x + ((int64_t)m * K + k) * (xbf ? 2 : 4));
-      }
+      // bf16 x needs two chunks per thread; the other two reload them (in bounds, unused).
+      const int c = t + 256 * (xbf ? (p & 1) : p);
+      const int row = xbf ? c >> 2 : c >> 3, kc = xbf ? (c & 3) * 8 : (c & 7) * 4;
+      const int m = min(m0 + row, M - 1);
+      const int k = min(k0 + kc, K - (xbf ? 8 : 4));
+      R.x[p] = *(const u32x4_v*)((const char*)a.x + ((int64_t)m * K + k) * (xbf ? 2 : 4));
     }
     const int k = min(k0 + wrow, K - 1);
     const char* wp = (const char*)a.w + ((int64_t)k * N + ncl) / (kI4 ? 2 : 1);
@@ -120,45 +136,41 @@ __global__ __launch_bounds__(kRgThreads, 2) void qdense_refgemm_kernel(RefGemmAr
     } else {
       R.w = *(const u32x4_v*)wp;
     }
-    const bool sbf = a.s_dt == MX_DTYPE_BFLOAT16, zbf = a.zp_dt == MX_DTYPE_BFLOAT16;
     if constexpr (SM == kRgCols) {
+      // 16 consecutive scales: four 16-byte loads of f32, two of bf16 (the other two repeat them).
       const int64_t si = (int64_t)(k / a.B) * N + ncl;
       const char* sp = (const char*)a.scale + si * (sbf ? 2 : 4);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        if (!sbf || q < 2) {
-          const u32x4_v v = *(const u32x4_v*)(sp + 16 * q);
+        const u32x4_v v = *(const u32x4_v*)(sp + 16 * (sbf ? (q & 1) : q));
 #pragma unroll
-          for (int e = 0; e < 4; ++e) R.s[4 * q + e] = v[e];
-        }
+        for (int e = 0; e < 4; ++e) R.s[4 * q + e] = v[e];
       }
       if (a.zp) {
         const char* zq = (const char*)a.zp + si * (zbf ? 2 : 4);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (!zbf || q < 2) {
-            const u32x4_v v = *(const u32x4_v*)(zq + 16 * q);
+          const u32x4_v v = *(const u32x4_v*)(zq + 16 * (zbf ? (q & 1) : q));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) R.z[4 * q + e] = v[e];
-          }
+          for (int e = 0; e < 4; ++e) R.z[4 * q + e] = v[e];
         }
       }
     } else if constexpr (SM == kRgBlk) {
       const int64_t si = (int64_t)k * a.nb + blo;
       const int64_t s2 = min<int64_t>(si + 1, (int64_t)k * a.nb + a.nb - 1);
-      R.s[0] = __float_as_uint(rg_load(a.scale, si, a.s_dt));
-      R.s[1] = __float_as_uint(rg_load(a.scale, s2, a.s_dt));
+      word(a.scale, si, sbf, R.s[0], R.ssh[0]);
+      word(a.scale, s2, sbf, R.s[1], R.ssh[1]);
       if (a.zp) {
-        R.z[0] = __float_as_uint(rg_load(a.zp, si, a.zp_dt));
-        R.z[1] = __float_as_uint(rg_load(a.zp, s2, a.zp_dt));
+        word(a.zp, si, zbf, R.z[0], R.zsh[0]);
+        word(a.zp, s2, zbf, R.z[1], R.zsh[1]);
       }
     } else {
       int b = blo, rem = ncl - blo * a.B;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t si = (int64_t)k * a.nb + b;
-        R.s[e] = __float_as_uint(rg_load(a.scale, si, a.s_dt));
-        if (a.zp) R.z[e] = __float_as_uint(rg_load(a.zp, si, a.zp_dt));
+        word(a.scale, si, sbf, R.s[e], R.ssh[e]);
+        if (a.zp) word(a.zp, si, zbf, R.z[e], R.zsh[e]);
         if (++rem == a.B) {
           rem = 0;
           ++b;
@@ -196,7 +208,7 @@ __global__ __launch_bounds__(kRgThreads, 2) void qdense_refgemm_kernel(RefGemmAr
       }
     }
     const bool ok = ncol_ok && k0 + wrow < K;
-    const bool sbf = a.s_dt == MX_DTYPE_BFLOAT16, zbf = a.zp_dt == MX_DTYPE_BFLOAT16;
+    const uint32_t smask = sbf ? 0xFFFF0000u : ~0u, zmask = zbf ? 0xFFFF0000u : ~0u;
     float v[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -215,11 +227,12 @@ __global__ __launch_bounds__(kRgThreads, 2) void qdense_refgemm_kernel(RefGemmAr
         if (a.zp)
           z = zbf ? __uint_as_float(e & 1 ? R.z[e >> 1] & 0xFFFF0000u : R.z[e >> 1] << 16) : __uint_as_float(R.z[e]);
       } else if constexpr (SM == kRgBlk) {
-        s = __uint_as_float(e < jsplit ? R.s[0] : R.s[1]);
-        if (a.zp) z = __uint_as_float(e < jsplit ? R.z[0] : R.z[1]);
+        s = e < jsplit ? __uint_as_float((R.s[0] << R.ssh[0]) & smask) : __uint_as_float((R.s[1] << R.ssh[1]) & smask);
+        if (a.zp)
+          z = e < jsplit ? __uint_as_float((R.z[0] << R.zsh[0]) & zmask) : __uint_as_float((R.z[1] << R.zsh[1]) & zmask);
       } else {
-        s = __uint_as_float(R.s[e]);
-        if (a.zp) z = __uint_as_float(R.z[e]);
+        s = __uint_as_float((R.s[e] << R.ssh[e]) & smask);
+        if (a.zp) z = __uint_as_float((R.z[e] << R.zsh[e]) & zmask);
       }
       const float ws = mul_rn(wf, s);
       v[e] = ok ? (a.zp ? add_rn(ws, z) : ws) : 0.0f;
@@ -305,13 +318,21 @@ int rg_mode(const QDenseDesc& d) {
   return d.block_size >= 16 ? kRgBlk : kRgAny;
 }
 
-template <int WDT>
+template <int WDT, bool PLAIN>
 void rg_dispatch(int mode, const RefGemmArgs& ra, int grid, hipStream_t st) {
   switch (mode) {
-    case kRgCols: dispatch(qdense_refgemm_kernel<WDT, kRgCols>, grid, kRgThreads, 0, st, ra); break;
-    case kRgBlk: dispatch(qdense_refgemm_kernel<WDT, kRgBlk>, grid, kRgThreads, 0, st, ra); break;
-    default: dispatch(qdense_refgemm_kernel<WDT, kRgAny>, grid, kRgThreads, 0, st, ra); break;
+    case kRgCols: dispatch(qdense_refgemm_kernel<WDT, kRgCols, PLAIN>, grid, kRgThreads, 0, st, ra); break;
+    case kRgBlk: dispatch(qdense_refgemm_kernel<WDT, kRgBlk, PLAIN>, grid, kRgThreads, 0, st, ra); break;
+    default: dispatch(qdense_refgemm_kernel<WDT, kRgAny, PLAIN>, grid, kRgThreads, 0, st, ra); break;
   }
+}
+
+template <int WDT>
+void rg_dispatch(int mode, bool plain, const RefGemmArgs& ra, int grid, hipStream_t st) {
+  if (plain)
+    rg_dispatch<WDT, true>(mode, ra, grid, st);
+  else
+    rg_dispatch<WDT, false>(mode, ra, grid, st);
 }
 
 }  // namespace
@@ -358,13 +379,14 @@ int qdense_refgemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ra.per_xcd = (int)((tiles + 7) / 8);
   const int grid = 8 * ra.per_xcd;
   const int mode = rg_mode(d);
+  const bool plain = d.x_dt == MX_DTYPE_FLOAT32 && !d.zp && d.scheme == MX_QUANT_LINEAR;
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     switch (d.w_dt) {
-      case MX_DTYPE_INT8: rg_dispatch<MX_DTYPE_INT8>(mode, ra, grid, st); break;
-      case MX_DTYPE_UINT8: rg_dispatch<MX_DTYPE_UINT8>(mode, ra, grid, st); break;
-      case MX_DTYPE_INT4: rg_dispatch<MX_DTYPE_INT4>(mode, ra, grid, st); break;
-      default: rg_dispatch<MX_DTYPE_UINT4>(mode, ra, grid, st); break;
+      case MX_DTYPE_INT8: rg_dispatch<MX_DTYPE_INT8>(mode, plain, ra, grid, st); break;
+      case MX_DTYPE_UINT8: rg_dispatch<MX_DTYPE_UINT8>(mode, plain, ra, grid, st); break;
+      case MX_DTYPE_INT4: rg_dispatch<MX_DTYPE_INT4>(mode, plain, ra, grid, st); break;
+      default: rg_dispatch<MX_DTYPE_UINT4>(mode, plain, ra, grid, st); break;
     }
   });
 }

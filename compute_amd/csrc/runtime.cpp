@@ -390,6 +390,9 @@ int mx_backend_finalize(mx_backend* b) {
     b->pending.clear();
     for (auto ev : b->event_cache) (void)hipEventDestroy(ev);
     b->event_cache.clear();
+    if (b->region_start) (void)hipEventDestroy(b->region_start);
+    if (b->region_stop) (void)hipEventDestroy(b->region_stop);
+    b->region_start = b->region_stop = nullptr;
     if (b->scratch) (void)hipFree(b->scratch);
     b->scratch = nullptr;
     b->pool.destroy();
@@ -495,6 +498,32 @@ int mx_backend_profile_reset(mx_backend* b) {
   std::lock_guard<std::recursive_mutex> lk(b->mu);
   MX_TRY(resolve_timings(b));
   b->prof.clear();
+  return MX_OK;
+}
+
+int mx_backend_region_begin(mx_backend* b) {
+  clear_error();
+  MX_TRY(check_device(b));
+  std::lock_guard<std::recursive_mutex> lk(b->mu);
+  if (!b->region_start) MX_CHECK_HIP(hipEventCreate(&b->region_start));
+  if (!b->region_stop) MX_CHECK_HIP(hipEventCreate(&b->region_stop));
+  MX_CHECK_HIP(hipEventRecord(b->region_start, b->stream));
+  b->region_open = true;
+  return MX_OK;
+}
+
+int mx_backend_region_end(mx_backend* b, double* ms) {
+  clear_error();
+  MX_TRY(check_device(b));
+  if (!ms) return set_error(MX_ERR_INVALID, "mx_backend_region_end: ms is NULL");
+  std::lock_guard<std::recursive_mutex> lk(b->mu);
+  if (!b->region_open) return set_error(MX_ERR_INVALID, "mx_backend_region_end: no region begun");
+  b->region_open = false;
+  MX_CHECK_HIP(hipEventRecord(b->region_stop, b->stream));
+  MX_CHECK_HIP(hipEventSynchronize(b->region_stop));
+  float f = 0.0f;
+  MX_CHECK_HIP(hipEventElapsedTime(&f, b->region_start, b->region_stop));
+  *ms = f;
   return MX_OK;
 }
 

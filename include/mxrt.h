@@ -190,6 +190,13 @@ int mx_backend_profile_entry(mx_backend* b, int i, char* name, size_t namelen, i
                              double* total_ms);
 int mx_backend_profile_reset(mx_backend* b);
 
+/* Timing of a stretch of queued work (benchmark harness; no reference counterpart): begin
+ * records an event on the backend's stream; end records a second one, waits for it and returns
+ * the device time between them in milliseconds.  Unlike the per-launch profile, nothing is added
+ * between the kernels, so back-to-back launches run as they would untimed. */
+int mx_backend_region_begin(mx_backend* b);
+int mx_backend_region_end(mx_backend* b, double* ms);
+
 /* Host-side fault injection (no reference counterpart; failure-path tests): the n-th device
  * allocation from now fails with MX_ERR_OUT_OF_MEMORY (n <= 0 disables). */
 int mx_backend_debug_fail_alloc_after(mx_backend* b, int n);
