@@ -24,6 +24,8 @@ Weight sets are handed out in one rotation across the warm-up, timed and event-t
 no loop starts on a set that is still in the Infinity Cache.
 `traffic` (HBM bytes per launch) is read from profiles/traffic.json, which is produced from
 rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this script (see --copy-calibration).
+`stream_floor` is a read-only pass over the headline's weight bytes (same rotation, same region
+timing): the HBM floor that the decode kernel's time is set beside.
 `cpu_baseline` times the CPU restatement of the reference loop (oracle/, the reference itself is
 Go and cannot be built here) on a bounded sample on this host.
 """
@@ -108,6 +110,29 @@ def measure(backend, wl, steps: int, warmup: int, rotate_bytes: int = 2 * MALL_B
     return {"ms_per_step": wall / steps * 1e3, "kernel": kname, "kernel_us": kernel_us, "kernel_us_source": source,
             "kernels": kernels, "kernel_us_per_step": kernel_us_per_step, "region_us_per_step": region_us,
             "weight_sets": n_sets}
+
+
+def stream_floor(backend, wl, steps: int, warmup: int, rotate_bytes: int = 2 * MALL_BYTES):
+    """The HBM streaming floor for the workload's weight bytes: read-only passes
+    (mx_backend_debug_stream_read, 16-byte loads, nothing written) over as many distinct weight
+    copies as the timed loop rotates through, `steps` passes timed as one region like the kernel."""
+    import compute_amd as ca
+
+    n_sets = max(1, math.ceil(rotate_bytes / wl.weight_bytes()))
+    bufs = [backend.BufferFromFlatData(0, wl.w.ravel(), ca.Shape(wl.w_dtype, wl.K, wl.N)) for _ in range(n_sets)]
+    backend.DebugStreamRead(bufs, warmup)
+    backend.Synchronize()
+    k = warmup % n_sets  # continue the rotation: the first timed pass reads the least recent copy
+    backend.RegionBegin()
+    backend.DebugStreamRead(bufs[k:] + bufs[:k], steps)
+    us = backend.RegionEnd() / steps * 1e3
+    for b in bufs:
+        b.Finalize()
+    nbytes = wl.weight_bytes()
+    return {"kernel": "stream_read_kernel", "bytes": nbytes, "us": round(us, 3),
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "us_at_algorithmic_bytes": round(us * wl.algorithmic_bytes() / nbytes, 3), "copies": n_sets,
+            "source": "hip_events_region"}
 
 
 def traffic_for(name: str):
@@ -346,6 +371,7 @@ def main():
                    "kernel": r["kernel"],
                    "tflops": round(wl.flops() / (r["ms_per_step"] * 1e-3) / 1e12, 3)},
         "roofline": hbm_roofline(nbytes, r["kernel_us"], traffic_for(wl.name)),
+        "stream_floor": stream_floor(backend, wl, args.steps, args.warmup),
     }
     extra = {}
     for name in [n for n in args.extra.split(",") if n]:

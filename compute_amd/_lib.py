@@ -107,6 +107,7 @@ SIGNATURES = {
     "mx_backend_profile_reset": [_P],
     "mx_backend_debug_fail_alloc_after": [_P, _I],
     "mx_backend_debug_noalloc_scratch": [_P, C.POINTER(_P)],
+    "mx_backend_debug_stream_read": [_P, C.POINTER(_P), _I, _I, _I],
     "mx_backend_region_begin": [_P],
     "mx_backend_region_end": [_P, C.POINTER(C.c_double)],
     "mx_backend_has_shared_buffers": [_P, C.POINTER(_I)],

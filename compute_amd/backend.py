@@ -382,6 +382,11 @@ class Backend:
         _check(self._lib.mx_backend_region_end(self._h, C.byref(ms)))
         return ms.value
 
+    def DebugStreamRead(self, bufs, passes: int, workgroups: int = 0) -> None:
+        """Queues `passes` read-only passes, pass i over bufs[i % len(bufs)] (HBM streaming floor)."""
+        arr = (C.c_void_p * len(bufs))(*[b._h for b in bufs])
+        _check(self._lib.mx_backend_debug_stream_read(self._h, arr, len(bufs), int(passes), int(workgroups)))
+
     def DebugNoAllocScratch(self) -> int:
         """Device address of the static array mx_qdense_noalloc uses on this backend's GPU."""
         p = C.c_void_p()

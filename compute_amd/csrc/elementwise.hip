@@ -8,6 +8,7 @@
 //   - ReduceSum on bf16/f16 accumulates in f32 and rounds at the end (reduce.go:416-437);
 //   - ConvertDType float -> bf16 uses round-to-nearest-even (bfloat16.go:30-39).
 
+#include <algorithm>
 #include <type_traits>
 
 #include "device_common.h"
@@ -589,3 +590,65 @@ int ew_rmsnorm(mx_backend* b, const void* x, const void* c, const void* e, void*
 }
 
 }  // namespace mx
+
+// ------------------------------------------------------------------------------------------
+// Read-only streaming pass (measurement): the HBM floor that a weight-streaming kernel of the
+// same byte count is compared with.  Grid-stride 16-byte nontemporal loads, eight in flight per
+// thread; the loaded words are folded into one value that an empty asm statement consumes, so
+// no load is removed and nothing is stored.
+// ------------------------------------------------------------------------------------------
+namespace mx {
+namespace {
+
+typedef uint32_t sr_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kStreamUnroll = 8;
+
+__global__ __launch_bounds__(256) void stream_read_kernel(const sr_u32x4* __restrict__ p, size_t n) {
+  const size_t nt = (size_t)gridDim.x * blockDim.x;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t h = 0;
+  for (; i + (kStreamUnroll - 1) * nt < n; i += kStreamUnroll * nt) {
+    sr_u32x4 v[kStreamUnroll];
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) v[u] = __builtin_nontemporal_load(p + i + u * nt);
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u) h ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  for (; i < n; i += nt) {
+    const sr_u32x4 v = __builtin_nontemporal_load(p + i);
+    h ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  asm volatile("" ::"v"(h));
+}
+
+}  // namespace
+}  // namespace mx
+
+extern "C" int mx_backend_debug_stream_read(mx_backend* b, const mx_buffer* const* bufs, int32_t nbufs,
+                                            int32_t passes, int32_t workgroups) {
+  mx::clear_error();
+  MX_TRY(mx::check_device(b));
+  if (!bufs || nbufs <= 0) return mx::set_error(MX_ERR_INVALID, "mx_backend_debug_stream_read: no buffers");
+  if (passes < 0 || workgroups < 0)
+    return mx::set_error(MX_ERR_INVALID, "mx_backend_debug_stream_read: negative passes or workgroups");
+  for (int32_t i = 0; i < nbufs; ++i) {
+    const mx_buffer* buf = bufs[i];
+    if (!buf) return mx::set_error(MX_ERR_INVALID, "mx_backend_debug_stream_read: buffer %d is NULL", i);
+    if (buf->finalized)
+      return mx::set_error(MX_ERR_FINALIZED, "mx_backend_debug_stream_read: buffer %d is finalized", i);
+    if (buf->b != b) return mx::set_error(MX_ERR_INVALID, "mx_backend_debug_stream_read: buffer %d of another backend", i);
+    if ((reinterpret_cast<uintptr_t>(buf->dptr) & 15) != 0)
+      return mx::set_error(MX_ERR_INVALID, "mx_backend_debug_stream_read: buffer %d not 16-byte aligned", i);
+  }
+  const unsigned grid = workgroups > 0 ? (unsigned)workgroups : 16u * (unsigned)std::max(b->num_cus, 1);
+  std::lock_guard<std::recursive_mutex> lk(b->mu);
+  for (int32_t p = 0; p < passes; ++p) {
+    const mx_buffer* buf = bufs[p % nbufs];
+    const size_t n = buf->nbytes / 16;
+    if (n == 0) continue;
+    MX_TRY(mx::launch(b, "stream_read", [&] {
+      mx::dispatch(mx::stream_read_kernel, grid, 256, 0, b->stream, (const mx::sr_u32x4*)buf->dptr, n);
+    }));
+  }
+  return MX_OK;
+}

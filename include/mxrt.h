@@ -204,6 +204,14 @@ int mx_backend_debug_fail_alloc_after(mx_backend* b, int n);
  * mx_qdense_noalloc uses on this backend's GPU (NULL for a host_only backend).  Backends on one
  * GPU report the same address. */
 int mx_backend_debug_noalloc_scratch(const mx_backend* b, void** out);
+/* Measurement aid (no reference counterpart; benchmark harness): queues `passes` read-only
+ * passes on the backend's stream, pass i over the storage of bufs[i % nbufs] (16-byte loads,
+ * whole 16-byte words only; nothing is written), each with the given number of 256-thread
+ * workgroups (0: 16 per CU).  A pass's duration is the HBM streaming floor for that many bytes,
+ * the figure a weight-streaming kernel is priced against beside the 8 TB/s peak; rotating over
+ * buffers larger together than the 256 MB Infinity Cache keeps the passes reading HBM. */
+int mx_backend_debug_stream_read(mx_backend* b, const mx_buffer* const* bufs, int32_t nbufs, int32_t passes,
+                                 int32_t workgroups);
 
 /* ---------------------------------------------------------------------------------------------
  * Buffers  —  compute.DataInterface (buffer.go:45-61) and compute.Buffer (buffer.go:12-43).

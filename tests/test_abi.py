@@ -58,6 +58,8 @@ def test_device_operations_fail_loudly_host_only(host_backend):
         host_backend.BufferFromFlatData(0, np.zeros(4, np.float32), ca.Shape(ca.Float32, 4))
     with pytest.raises(ca.ErrNoDevice):
         host_backend.Synchronize()
+    with pytest.raises(ca.ErrNoDevice):
+        host_backend.DebugStreamRead([], 1)
 
 
 def _qd_builder(b, xs, ws, ss, bias_shape=None):

@@ -207,3 +207,33 @@ def test_bitcast_uint8_to_int4_kat(backend, key, donate):
         assert np.array_equal(o.ToFlatData(), src)
     assert np.array_equal(O.unpack_int4(outs[1].ToFlatData(), signed=True),
                           [((b >> s & 15) ^ 8) - 8 for b in src.tolist() for s in (0, 4)])
+
+
+# ---------------------------------------------------------------------------------------------
+# Measurement hooks of the benchmark (no reference counterpart): the streaming-floor pass rotates
+# over its buffers, writes nothing, shows in the per-kernel profile and in a timed region, and
+# rejects finalized buffers.
+# ---------------------------------------------------------------------------------------------
+def test_stream_read_measurement_hook(backend):
+    rng = np.random.default_rng(3)
+    data = [rng.integers(0, 256, (1 << 20) + 40, dtype=np.uint8) for _ in range(2)]
+    bufs = [backend.BufferFromFlatData(0, d, Shape(DType.Uint8, d.size)) for d in data]
+    backend.SetProfiling(True)
+    backend.ProfileReset()
+    try:
+        backend.RegionBegin()
+        backend.DebugStreamRead(bufs, 3, 64)
+        backend.DebugStreamRead(bufs, 2)
+        assert backend.RegionEnd() > 0
+        prof = backend.Profile()
+    finally:
+        backend.SetProfiling(False)
+    assert prof["stream_read"][0] == 5
+    for b, d in zip(bufs, data):
+        assert np.array_equal(b.ToFlatData(), d)
+    backend.DebugStreamRead(bufs, 0)
+    bufs[1].Finalize()
+    with pytest.raises(B.ErrFinalized):
+        backend.DebugStreamRead(bufs, 1)
+    with pytest.raises(B.ComputeError):
+        backend.DebugStreamRead([bufs[0]], -1)
