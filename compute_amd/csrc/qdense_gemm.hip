@@ -9,31 +9,31 @@
 // with one group for per-channel scales; every product x*w is exact in f32 (bf16 x, |w| < 256),
 // so only the summation order differs from the reference.  With groups, the MFMAs of a group
 // accumulate into a second set of registers that is folded into the total with the group's
-// scales (acc += accg * s[g]) at the group's last block; to leave room for that set, a grouped
-// workgroup's tile is 256 x 64, each wave keeping two of the four interleaved column sets
-// (columns 4*cg + 2*wc + c of the Bt tile, read with the same swizzles).
+// scales (acc += accg * s[g]) at the group's last block.
 //
 // Tiling.  A workgroup (8 waves, two per SIMD) computes a 256 x 128 output tile; wave w owns
 // rows [64 wr, 64 wr + 64) x columns [64 wc, 64 wc + 64) with wr = w % 4, wc = w / 4.  K advances
-// in blocks of 64 (two 32-row steps of v_mfma_f32_16x16x32_bf16).  LDS holds two buffers of
-//   - x: [256 rows][64 k] bf16; 16-byte k-chunks XOR-swizzled within each row by (row >> 1) & 7
-//     so that an MFMA operand read (16 rows) hits distinct banks;
-//   - Bt: [128 columns][64 k] bf16, the weights converted exactly to bf16 (|w| < 256 has at most
-//     8 significant bits) and transposed.  Column c is stored in row p = c ^ ((c >> 2) & 1)
-//     and its 16-byte k-chunks are XOR-swizzled by (p >> 3) & 7: the 16 lanes of a B-operand read
-//     (columns 4 apart) then cover both halves of the banks and 8 distinct chunks in each.
-// Block kb runs its MFMAs from buffer kb % 2 while the workgroup's loads of block kb + 4 travel
-// into registers (four blocks of lead cover an L2 miss) and block kb + 1, loaded earlier, is
-// written into the
-// other buffer: each thread loads 4 x 16 bytes of x (8 threads per 128-byte row segment) and
-// 4 rows x 4 columns of 8-bit weights (32 threads per 128-byte row segment) or 2 rows x 8
-// columns of 4-bit weights (16 threads per 64-byte row segment) per block.  One barrier per block publishes the next buffers and retires the reads
-// of the current ones; it sits between the block's two steps, so that the next block's step-0
-// operand reads travel under step 1's MFMAs.  Every access is compiler-visible (the compiler
-// places the waits), and sched_group_barrier interleaves the memory instructions one per MFMA:
-// issuing a global load or an LDS access can stall the wave (the CU's vector-memory path takes
-// 40 KB per block, and LDS writes run at about 90 bytes/clock per CU), and a stall that overlaps
-// an MFMA in flight costs nothing.  Loads past the last block re-read it (clamped index).
+// in blocks of 64 (two 32-row steps of v_mfma_f32_16x16x32_bf16).  LDS holds
+//   - x, three buffers: [256 rows][64 k] bf16; 16-byte k-chunks XOR-swizzled within each row by
+//     (row >> 1) & 7 so that an MFMA operand read (16 rows) hits distinct banks;
+//   - Bt, two buffers: [128 columns][64 k] bf16, the weights converted exactly to bf16 (|w| < 256
+//     has at most 8 significant bits) and transposed.  Column c is stored in row p = c ^ ((c >> 2)
+//     & 1) and its 16-byte k-chunks are XOR-swizzled by (p >> 3) & 7: the 16 lanes of a B-operand
+//     read (columns 4 apart) then cover both halves of the banks and 8 distinct chunks in each.
+// x moves straight from memory into its LDS buffer (global_load_lds_dwordx4, 1 KB = 8 rows per
+// wave instruction, the swizzle applied by choosing each lane's source chunk) two blocks ahead of
+// its use, and takes no registers, VALU or LDS-write instructions; that leaves room for the
+// grouped kernels' second accumulator set beside a full 256 x 128 tile.  The weights travel
+// through registers (loads of block kb + PF issued during block kb, each thread 4 rows x 4
+// columns: 4 bytes of int8, 2 of 4-bit or 8 of a half type per row; 32 threads per row segment),
+// are converted and written transposed into the Bt buffer of block kb + 1 during block kb.
+// One barrier per block publishes the next block (each wave first waits for its own x loads of
+// it: the loads are issued in a fixed order, so a count of outstanding loads names them) and
+// retires the reads of the current buffers; it sits between the block's two steps, so that the
+// next block's step-0 operand reads travel under step 1's MFMAs.  sched_group_barrier interleaves
+// the memory instructions one per MFMA: issuing a global load or an LDS access can stall the
+// wave, and a stall that overlaps an MFMA in flight costs nothing.  Loads past the last block
+// re-read it (clamped index), which keeps the count of loads per block fixed.
 // Lane (cg = lane % 16, kq = lane / 16) ends with rows 4*kq + r of each 16-row block and the 4
 // consecutive columns 4*cg .. 4*cg + 3 of its wave's 64; the epilogue applies scale, bias and
 // activation and writes 8-byte bf16 runs.
@@ -56,13 +56,13 @@ typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
 constexpr int kBM = 256, kBN = 128, kBK = 64, kWaves = 8, kThreads = 64 * kWaves;
 constexpr int kABytes = kBM * kBK * 2;   // 32 KB per x buffer
 constexpr int kBtBytes = kBN * kBK * 2;  // 16 KB per Bt buffer
-constexpr int kLds = 2 * kABytes + 2 * kBtBytes;
-constexpr int kXLoads = kABytes / (kThreads * 16);  // 16-byte x loads per thread per block
-constexpr int kWLoads = 4;                           // w loads (4 bytes) per thread per block
-constexpr int kPf = 4;                               // blocks loaded ahead into registers
-constexpr int kPfGrouped = 4;                        // the same with scale groups
-constexpr int kUnroll = 4;                           // multiple of kPf and of the 2 LDS buffers
-static_assert(kXLoads * kThreads * 16 == kABytes, "x load split");
+constexpr int kXBufs = 3;                            // x buffers: a block's rows land two blocks ahead
+constexpr int kXDma = kABytes / (kWaves * 1024);     // 1 KB direct-to-LDS loads per wave per block
+constexpr int kWLoads = 4;                           // w loads (one per row) per thread per block
+constexpr int kPf = 4;                               // w blocks loaded ahead into registers
+constexpr int kPfGrouped = 2;                        // the same with scale groups
+constexpr int kUnroll = 4;                           // multiple of kPf and of the 2 Bt buffers
+static_assert(kXDma * kWaves * 1024 == kABytes, "x load split");
 static_assert(kBK * kBN == 16 * kThreads, "conversion: 16 weights per thread");
 
 // B operand kinds: the quantized weights [K, N] (int8 / uint8, converted to bf16), or a
@@ -99,6 +99,41 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// LDS byte address of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Direct memory-to-LDS load of 16 bytes per lane from base + voff (base wave-uniform, voff the
+// lane's byte offset): lane l's bytes land at LDS address lds_base + 16 * l (lds_base
+// wave-uniform, held in M0 for the instruction, which is saved and restored around it).  Issued as assembly: the compiler neither waits for it nor knows that it
+// writes LDS, so the kernel waits for it itself (wait_vm) before the barrier that publishes the
+// block, and the "memory" clobber keeps every compiler memory access in program order around it.
+// The memory counter completes loads in issue order, so the compiler's own waits for its later
+// or earlier loads stay correct (they only cover these as well).
+__device__ __forceinline__ void lds_dma_b128(const void* base, uint32_t voff, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(lds_base), "s"(base)
+      : "memory");
+}
+
+// Waits until at most N of this wave's memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N == 6 || N == 8, "counts used by the kernel");
+  if constexpr (N == 6)
+    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 }
 
 typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
@@ -144,8 +179,8 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // With scale groups the tile is 256 x 64: each wave keeps two of the four interleaved MFMA
   // column sets (columns 4*cg + 2*wc + c, c = 0, 1), which halves both accumulator sets so that
   // the second one fits beside the operands without spilling.
-  constexpr int BN = GRP ? kBN / 2 : kBN;
-  constexpr int NC = GRP ? 2 : 4;  // MFMA column sets per wave
+  constexpr int BN = kBN;
+  constexpr int NC = 4;  // MFMA column sets per wave
   static_assert(kUnroll % PF == 0, "register slots cycle within the unroll");
   // Tile order: consecutive work items go to one XCD (workgroups are dispatched round-robin over
   // the 8); with whole 2 x 16 tile groups, 32 consecutive items form one group.  DotGeneral
@@ -176,52 +211,42 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   const int KB = a.K / kBK;
   const size_t N = (size_t)a.N;
 
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kABytes];
+  __shared__ __attribute__((aligned(16))) uint8_t xs[kXBufs][kABytes];
   __shared__ __attribute__((aligned(16))) uint8_t bt[2][kBtBytes];
 
-  // x: thread t loads chunks q = t + kThreads * i: row q / 8, k-chunk q % 8 (16 bytes), stored at
-  // chunk (q % 8) ^ ((row >> 1) & 7) of the row.  Rows past M read row M-1.
+  // x: each wave moves kXDma 1 KB pieces of a block straight into LDS: piece q = kXDma*wave + i
+  // holds rows 8q .. 8q + 7 (128 bytes each); lane l lands at row 8q + l / 8, 16-byte slot
+  // l % 8, which holds the row's k-chunk (l % 8) ^ ((row >> 1) & 7).  Rows past M read row M-1.
   const int t = threadIdx.x;
-  const uint16_t* xsrc[kXLoads];
-  uint32_t xdst[kXLoads];
+  // Byte offsets from the block's start in x (M * K < 2^31 elements, checked by the host).
+  uint32_t xoff[kXDma];
 #pragma unroll
-  for (int i = 0; i < kXLoads; ++i) {
-    const int q = t + kThreads * i;
-    const int r = q >> 3, c = q & 7;
-    xsrc[i] = a.x + (size_t)min(m0 + r, a.M - 1) * a.K + 8 * c;
-    xdst[i] = (uint32_t)(r * (kBK * 2) + ((c ^ ((r >> 1) & 7)) << 4));
+  for (int i = 0; i < kXDma; ++i) {
+    const int r = 8 * (kXDma * wave + i) + (lane >> 3);
+    xoff[i] = 2u * ((uint32_t)min(m0 + r, a.M - 1) * (uint32_t)a.K + 8u * ((lane & 7) ^ ((r >> 1) & 7)));
   }
-  auto load_x = [&](int kb, u32x4_v (&dst)[kXLoads]) {
+  const uint32_t xs_lds = lds_addr(&xs[0][0]) + (uint32_t)(kXDma * wave) * 1024u;
+  auto dma_x = [&](int kb) {
+    const uint32_t dst = xs_lds + (uint32_t)(kb % kXBufs) * kABytes;
     kb = min(kb, KB - 1);
 #pragma unroll
-    for (int i = 0; i < kXLoads; ++i) dst[i] = *(const u32x4_v*)(xsrc[i] + (size_t)kb * kBK);
+    for (int i = 0; i < kXDma; ++i) lds_dma_b128(a.x + (size_t)kb * kBK, xoff[i], dst + 1024u * i);
   };
-  auto store_x = [&](const u32x4_v (&v)[kXLoads], int buf) {
-#pragma unroll
-    for (int i = 0; i < kXLoads; ++i) *(u32x4_v*)(&xs[buf][xdst[i]]) = v[i];
-  };
-  // B, [K, N] kinds: thread t converts columns 4*cq .. 4*cq + 3 and rows 4*j .. 4*j + 3 of each
-  // block; the 32 threads of a j read one contiguous row segment (128 bytes of int8, 256 of a
-  // half type).  Columns past N read column 0 (their outputs are not stored).
+  // B, [K, N] kinds: thread t (cq = t % 32, j = t / 32) converts columns 4*cq .. 4*cq + 3 and
+  // rows 4*j .. 4*j + 3 of each block; the 32 threads of a j read one contiguous row segment
+  // (128 bytes of int8, 64 of 4-bit, 256 of a half type).  Columns past N read column 0 (their
+  // outputs are not stored).
   // [N, K] kinds: B rows are k-contiguous like x: thread t copies 16-byte chunks q = t + kThreads*i,
   // column q / 8 (rows past N read row N-1), k-chunk q % 8.
-  // 4-bit kinds: thread t converts columns 8*cq .. 8*cq + 7 and rows 2*j, 2*j + 1 of each block
-  // (cq = t % 16, j = t / 16); the 16 threads of a j read one 64-byte row segment.
-  constexpr int kEB = kDotB<BK> ? 2 : 1;  // bytes per B element
-  // Threads per row group of the B tile; with the 64-column tile the second half of the threads
-  // repeats the first half's rows (their loads hit the cache and they store nothing).
-  constexpr int kCQ = (k4B<BK> ? 16 : 32) * BN / kBN;
-  constexpr int kJ = kThreads * BN / kBN / kCQ;  // row groups of one block
-  const int cq = t % kCQ, jt = t / kCQ, j = jt % kJ;
-  const bool b_store = jt < kJ;
-  const int cpt = k4B<BK> ? 8 : 4;  // columns per thread
-  const int wcol = n0 + cpt * cq + cpt <= a.N ? n0 + cpt * cq : 0;
-  const uint8_t* wsrc = k4B<BK> ? a.w + ((size_t)(2 * j) * N + wcol) / 2 : a.w + ((size_t)(4 * j) * N + wcol) * kEB;
-  // Column 4*cq + c lives in Bt row (4*cq + c) ^ (cq & 1), k-chunk j / 2 swizzled by (cq / 2) & 7.
-  // 4-bit: column 8*cq + c in Bt row (8*cq + c) ^ ((c >> 2) & 1), k-chunk j / 4 swizzled by cq & 7,
-  // 4-byte pair (rows 2j, 2j + 1) j % 4 of the chunk.
-  const uint32_t cv_off = k4B<BK> ? (uint32_t)((((j >> 2) ^ (cq & 7)) << 4) + ((j & 3) << 2))
-                                  : (uint32_t)((((j >> 1) ^ ((cq >> 1) & 7)) << 4) + ((j & 1) << 3));
+  constexpr int kCQ = 32, kJ = kThreads / kCQ;  // threads per row group, row groups of one block
+  static_assert(4 * kJ == kBK && 4 * kCQ == kBN, "B conversion split");
+  const int cq = t % kCQ, j = t / kCQ;
+  const int wcol = n0 + 4 * cq + 4 <= a.N ? n0 + 4 * cq : 0;
+  const uint8_t* wsrc = k4B<BK> ? a.w + ((size_t)(4 * j) * N + wcol) / 2
+                                : a.w + ((size_t)(4 * j) * N + wcol) * (kDotB<BK> ? 2 : 1);
+  // Column 4*cq + c lives in Bt row (4*cq + c) ^ (cq & 1), k-chunk j / 2 swizzled by (cq / 2) & 7,
+  // 8-byte half j % 2 of the chunk.
+  const uint32_t cv_off = (uint32_t)((((j >> 1) ^ ((cq >> 1) & 7)) << 4) + ((j & 1) << 3));
   constexpr int kNKLoads = kBtBytes / (kThreads * 16);
   const uint8_t* nksrc[kNKLoads];
   uint32_t nkdst[kNKLoads];
@@ -235,7 +260,8 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     }
   }
   // Register words of one block of B per thread.
-  constexpr int kWWords = kNKB<BK> ? 4 * kNKLoads : (kDotB<BK> ? 2 * kWLoads : (k4B<BK> ? 2 : kWLoads));
+  constexpr int kWWords = kNKB<BK> ? 4 * kNKLoads : (kDotB<BK> ? 2 * kWLoads : kWLoads);
+  constexpr int kWWrites = kNKB<BK> ? kNKLoads : 4;  // Bt writes per thread per block
   auto load_w = [&](int kb, uint32_t (&dst)[kWWords]) {
     kb = min(kb, KB - 1);
     if constexpr (kNKB<BK>) {
@@ -254,35 +280,18 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       }
     } else if constexpr (k4B<BK>) {
 #pragma unroll
-      for (int e = 0; e < 2; ++e)
-        dst[e] = __builtin_nontemporal_load((const uint32_t*)(wsrc + (size_t)(kb * kBK + e) * (N / 2)));
+      for (int e = 0; e < kWLoads; ++e)
+        dst[e] = __builtin_nontemporal_load((const uint16_t*)(wsrc + (size_t)(kb * kBK + e) * (N / 2)));
     } else {
 #pragma unroll
       for (int e = 0; e < kWLoads; ++e)
         dst[e] = __builtin_nontemporal_load((const uint32_t*)(wsrc + (size_t)(kb * kBK + e) * N));
     }
   };
-  // Four k-values of each of four consecutive columns (Bt rows 128 bytes apart): int8 converted
-  // exactly to bf16, half values regrouped by column.  [N, K]: the chunks as loaded.
+  // Four k-values of each of four consecutive columns (Bt rows 128 bytes apart): int8 and 4-bit
+  // converted exactly to bf16, half values regrouped by column.  [N, K]: the chunks as loaded.
   auto store_w = [&](const uint32_t (&w4)[kWWords], int buf) {
-    if (GRP && !b_store) return;
-    if constexpr (k4B<BK>) {
-      // Nibble c of each row word is column 8*cq + c (reference packing: low nibble first);
-      // both rows converted exactly through f32 and packed as a bf16 pair.
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        float f[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          if constexpr (BK == kBI4)
-            f[e] = (float)((int32_t)(w4[e] << (28 - 4 * c)) >> 28);
-          else
-            f[e] = (float)((w4[e] >> (4 * c)) & 15u);
-        }
-        const uint32_t v = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
-        *(uint32_t*)(&bt[buf][cv_off + (uint32_t)((8 * cq + (c ^ ((c >> 2) & 1))) * (kBK * 2))]) = v;
-      }
-    } else if constexpr (kNKB<BK>) {
+    if constexpr (kNKB<BK>) {
 #pragma unroll
       for (int i = 0; i < kNKLoads; ++i)
         *(u32x4_v*)(&bt[buf][nkdst[i]]) = u32x4_v{w4[4 * i], w4[4 * i + 1], w4[4 * i + 2], w4[4 * i + 3]};
@@ -301,8 +310,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
           for (int e = 0; e < 4; ++e) {
             if constexpr (BK == kBI8)
               f[e] = (float)(int8_t)(w4[e] >> (8 * c));
-            else
+            else if constexpr (BK == kBU8)
               f[e] = (float)(uint8_t)(w4[e] >> (8 * c));
+            else if constexpr (BK == kBI4)  // nibble c, low nibble first (reference packing)
+              f[e] = (float)((int32_t)(w4[e] << (28 - 4 * c)) >> 28);
+            else
+              f[e] = (float)((w4[e] >> (4 * c)) & 15u);
           }
           v = u32x2_v{__builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u),
                       __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u)};
@@ -320,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     for (int c = 0; c < NC; ++c) acc[rb][c] = accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // Grouped scales: this lane's 4 columns' scales of the group being summed, loaded a group ahead.
   // This lane's first column: 64*wc + 4*cg (four consecutive), or 4*cg + 2*wc (two) with groups.
-  const int lcol = GRP ? n0 + 4 * cg + 2 * wc : n0 + 64 * wc + 4 * cg;
+  const int lcol = n0 + 64 * wc + 4 * cg;
   const int scol = min(lcol, a.N - NC);
   float sg[NC];
 #pragma unroll
@@ -335,17 +348,17 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // MFMA operands of one 32-row step: x row 64*wr + 16*rb + cg, Bt column 64*wc + 4*cg + c (Bt
   // row 64*wc + 4*cg + (c ^ (cg & 1))); with groups, Bt column 4*cg + 2*wc + c.
   const uint32_t a_row = (uint32_t)((64 * wr + cg) * (kBK * 2));
-  const uint32_t b_col = (uint32_t)(((GRP ? 0 : 64 * wc) + 4 * cg) * (kBK * 2));
-  const int b_par = cg & 1, c_base = GRP ? 2 * wc : 0;
+  const uint32_t b_col = (uint32_t)((64 * wc + 4 * cg) * (kBK * 2));
+  const int b_par = cg & 1;
   // Operands of one 32-row step (sub = 0, 1 of a block) from LDS buffer buf, and its 16 MFMAs.
-  auto read_step = [&](int buf, int sub, u32x4_v (&A)[4], u32x4_v (&B)[NC]) {
+  auto read_step = [&](int xbuf, int buf, int sub, u32x4_v (&A)[4], u32x4_v (&B)[NC]) {
     const int kc = 4 * sub + kq;  // 16-byte k-chunk of this lane
-    const uint8_t* ap = &xs[buf][a_row + ((kc ^ (cg >> 1)) << 4)];
+    const uint8_t* ap = &xs[xbuf][a_row + ((kc ^ (cg >> 1)) << 4)];
     const uint8_t* bp = &bt[buf][b_col + ((kc ^ ((cg >> 1) & 7)) << 4)];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) A[rb] = *(const u32x4_v*)(ap + rb * 16 * (kBK * 2));
 #pragma unroll
-    for (int c = 0; c < NC; ++c) B[c] = *(const u32x4_v*)(bp + ((c_base + c) ^ b_par) * (kBK * 2));
+    for (int c = 0; c < NC; ++c) B[c] = *(const u32x4_v*)(bp + (c ^ b_par) * (kBK * 2));
   };
   auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[NC], auto first) __attribute__((always_inline)) {
 #pragma unroll
@@ -373,52 +386,59 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     load_sg(g + 1);
   };
 
-  // Register slots hold the next kPf blocks' x and w: block kb's slot is free once block kb
-  // is in LDS (written during block kb - 1), so block kb refills it with block kb + kPf and
-  // writes block kb + 1 into the other LDS buffer.  The order keeps the matrix cores fed while
-  // LDS traffic is in flight: on entry step 0's operands of block kb are in registers (A0, B0);
-  // step 1's reads and block kb + 1's writes are issued before step 0's MFMAs, and after the
-  // barrier that publishes block kb + 1, its step-0 reads are issued before step 1's MFMAs.
-  // (sched_barrier keeps the compiler from regrouping the phases.)
-  u32x4_v xr[PF][kXLoads];
+  // x moves by direct-to-LDS loads two blocks ahead of its use (three buffers: block kb's
+  // buffer takes block kb + 3 once its last operands are read, i.e. after block kb's barrier); w
+  // moves through register slots that hold the next PF blocks: block kb's slot is free once
+  // block kb is in LDS (written during block kb - 1), so block kb refills it with block kb + PF
+  // and writes block kb + 1 into the other Bt buffer.  The order keeps the matrix cores fed
+  // while LDS traffic is in flight: on entry step 0's operands of block kb are in registers (A0,
+  // B0); step 1's reads and block kb + 1's Bt writes are issued before step 0's MFMAs, and after
+  // the barrier that publishes block kb + 1 (its Bt writes and its x, whose loads this wave
+  // waits for first), its step-0 reads are issued before step 1's MFMAs.  Every step issues its
+  // loads in one order (w, then x), so the number of loads issued after a block's x loads is
+  // fixed: kWGl + kXDma when that block is published.  (sched_barrier keeps the compiler from
+  // regrouping the phases.)
+  constexpr int kWGl = kNKB<BK> ? kNKLoads : kWLoads;
+  static_assert(PF >= 2, "the prologue issues two blocks of w loads around the x loads");
   uint32_t wr4[PF][kWWords];
   u32x4_v A0[4], B0[NC], A1[4], B1[NC];
   auto block = [&](int kb, auto step) __attribute__((always_inline)) {
     constexpr int U = decltype(step)::value;  // kb % kUnroll
     constexpr int S = U % PF, S1 = (U + 1) % PF, B = U % 2;
+    const int xb = (int)((unsigned)kb % kXBufs), xb1 = xb == kXBufs - 1 ? 0 : xb + 1;
     // Step 0: its MFMAs interleaved with step 1's operand reads, then with the conversion and
     // LDS writes of block kb + 1, so that every issue stall of a memory instruction overlaps an
     // MFMA in flight.
-    read_step(B, 1, A1, B1);
-    store_x(xr[S1], B ^ 1);
+    read_step(xb, B, 1, A1, B1);
     store_w(wr4[S1], B ^ 1);
     mma_step(A0, B0, std::integral_constant<bool, GPB != 0 && U % (GPB ? GPB : 1) == 0>{});
 #pragma unroll
-    for (int i = 0; i < 2 * NC; ++i) {
+    for (int i = 0; i < 4 + NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
 #pragma unroll
-    for (int i = 0; i < 2 * NC; ++i) {
+    for (int i = 0; i < kWWrites; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
       __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
     __builtin_amdgcn_sched_barrier(0);
+    wait_vm<kWGl + kXDma>();  // this wave's x loads of block kb + 1 are in LDS
     lds_barrier();
-    // Step 1: its MFMAs interleaved with block kb + 1's step-0 reads and the global loads of
-    // block kb + kPf.
-    read_step(B ^ 1, 0, A0, B0);
-    load_x(kb + PF, xr[S]);
+    // Step 1: its MFMAs interleaved with block kb + 1's step-0 reads and the loads of block
+    // kb + PF (w) and kb + 3 (x).
+    read_step(xb1, B ^ 1, 0, A0, B0);
     load_w(kb + PF, wr4[S]);
+    dma_x(kb + kXBufs);
     mma_step(A1, B1, std::false_type{});
 #pragma unroll
-    for (int i = 0; i < 2 * NC; ++i) {
+    for (int i = 0; i < 4 + NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
 #pragma unroll
-    for (int i = 0; i < 2 * NC; ++i) {
+    for (int i = 0; i < kWGl; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
@@ -431,15 +451,19 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   };
   auto blocks = [&](int kb, int n, auto... steps) { ((steps.value < n ? block(kb + steps.value, steps) : void()), ...); };
 
+  // Prologue: the loads of blocks 0..2 (x) and 0..PF-1 (w) in the steady state's order (each x
+  // block after one block of w loads), then all of them waited for.
 #pragma unroll
-  for (int p = 0; p < PF; ++p) {
-    load_x(p, xr[p]);
-    load_w(p, wr4[p]);
-  }
-  store_x(xr[0], 0);
+  for (int p = 0; p + 2 < PF; ++p) load_w(p, wr4[p]);
+  dma_x(0);
+  load_w(PF - 2, wr4[PF - 2]);
+  dma_x(1);
+  load_w(PF - 1, wr4[PF - 1]);
+  dma_x(2);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   store_w(wr4[0], 0);
   lds_barrier();
-  read_step(0, 0, A0, B0);
+  read_step(0, 0, 0, A0, B0);
   int kb = 0;
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -473,50 +497,23 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
         }
       }
     return;
-  } else if constexpr (GRP) {
-    // Two consecutive columns per row (the scales were applied by fold()): bias, activation, bf16.
-    float bi[2];
+  } else {
+    float sc[4], bi[4];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) bi[c] = a.bias ? load_f(a.bias, ncol + c, a.b_dt) : 0.0f;
+    for (int c = 0; c < 4; ++c) {
+      sc[c] = GRP ? 1.0f : load_f(a.scale, ncol + c, a.s_dt);  // grouped: applied by fold()
+      bi[c] = a.bias ? load_f(a.bias, ncol + c, a.b_dt) : 0.0f;
+    }
     const int row0 = m0 + 64 * wr + 4 * kq;
     uint16_t* out = (uint16_t*)a.out;
-    auto store2 = [&](auto actc) __attribute__((always_inline)) {
-      constexpr int ACT = decltype(actc)::value;
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = row0 + 16 * rb + r;
-          if (row < a.M)
-            *(uint32_t*)(out + (size_t)row * N + ncol) =
-                scaled_act_bf16x2<ACT>(acc[rb][0][r], 1.0f, bi[0], acc[rb][1][r], 1.0f, bi[1]);
-        }
-    };
     switch (a.act) {
-      case MX_ACT_GELU: store2(std::integral_constant<int, MX_ACT_GELU>{}); break;
-      case MX_ACT_RELU: store2(std::integral_constant<int, MX_ACT_RELU>{}); break;
-      case MX_ACT_SILU: store2(std::integral_constant<int, MX_ACT_SILU>{}); break;
-      case MX_ACT_HARDSWISH: store2(std::integral_constant<int, MX_ACT_HARDSWISH>{}); break;
-      case MX_ACT_TANH: store2(std::integral_constant<int, MX_ACT_TANH>{}); break;
-      default: store2(std::integral_constant<int, MX_ACT_NONE>{}); break;
+      case MX_ACT_GELU: store_tile<MX_ACT_GELU>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+      case MX_ACT_RELU: store_tile<MX_ACT_RELU>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+      case MX_ACT_SILU: store_tile<MX_ACT_SILU>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+      case MX_ACT_HARDSWISH: store_tile<MX_ACT_HARDSWISH>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+      case MX_ACT_TANH: store_tile<MX_ACT_TANH>(acc, sc, bi, out, row0, a.M, N, ncol); break;
+      default: store_tile<MX_ACT_NONE>(acc, sc, bi, out, row0, a.M, N, ncol); break;
     }
-  } else {
-  float sc[4], bi[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    sc[c] = GRP ? 1.0f : load_f(a.scale, ncol + c, a.s_dt);  // grouped: applied by fold()
-    bi[c] = a.bias ? load_f(a.bias, ncol + c, a.b_dt) : 0.0f;
-  }
-  const int row0 = m0 + 64 * wr + 4 * kq;
-  uint16_t* out = (uint16_t*)a.out;
-  switch (a.act) {
-    case MX_ACT_GELU: store_tile<MX_ACT_GELU>(acc, sc, bi, out, row0, a.M, N, ncol); break;
-    case MX_ACT_RELU: store_tile<MX_ACT_RELU>(acc, sc, bi, out, row0, a.M, N, ncol); break;
-    case MX_ACT_SILU: store_tile<MX_ACT_SILU>(acc, sc, bi, out, row0, a.M, N, ncol); break;
-    case MX_ACT_HARDSWISH: store_tile<MX_ACT_HARDSWISH>(acc, sc, bi, out, row0, a.M, N, ncol); break;
-    case MX_ACT_TANH: store_tile<MX_ACT_TANH>(acc, sc, bi, out, row0, a.M, N, ncol); break;
-    default: store_tile<MX_ACT_NONE>(acc, sc, bi, out, row0, a.M, N, ncol); break;
-  }
   }
 }
 
@@ -531,7 +528,8 @@ bool qdense_gemm_fits(const QDenseDesc& d) {
                   d.w_dt == MX_DTYPE_UINT4;
   return d.M > 16 && d.x_dt == MX_DTYPE_BFLOAT16 && d.scheme == MX_QUANT_LINEAR && !d.zp && (per_channel || grouped) &&
          wt && d.K >= kBK && d.K % kBK == 0 && d.N >= 16 && d.N % 16 == 0 && d.M < (1 << 30) && d.K < (1 << 30) &&
-         d.N < (1 << 30) && aligned(d.w, 16) && aligned(d.x, 16) && aligned(d.out, 16);
+         d.N < (1 << 30) && d.M * d.K < ((int64_t)1 << 31) && aligned(d.w, 16) && aligned(d.x, 16) &&
+         aligned(d.out, 16);
 }
 
 int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
@@ -548,7 +546,8 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.b_dt = d.b_dt;
   ga.act = d.act;
   const bool grouped = d.block_size < d.K;
-  const int64_t bn = grouped ? kBN / 2 : kBN;  // the kernel's tile width (64 with scale groups)
+  // The kernel's tile width: 64 for 4-bit weights with scale groups.
+  const int64_t bn = kBN;
   const int64_t tiles_m = (d.M + kBM - 1) / kBM, tiles_n = (d.N + bn - 1) / bn;
   if (tiles_m * tiles_n > (int64_t)1 << 30)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: output too large for the GEMM path");
@@ -561,23 +560,19 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   return launch(b, name, [&] {
     switch (d.w_dt) {
       case MX_DTYPE_INT8:
-        grouped ? (ga.gpb == 2 ? dispatch(qdense_gemm_kernel<kBI8, true, 2>, grid, kThreads, 0, st, ga)
-                               : dispatch(qdense_gemm_kernel<kBI8, true>, grid, kThreads, 0, st, ga))
+        grouped ? dispatch(qdense_gemm_kernel<kBI8, true>, grid, kThreads, 0, st, ga)
                 : dispatch(qdense_gemm_kernel<kBI8, false>, grid, kThreads, 0, st, ga);
         break;
       case MX_DTYPE_UINT8:
-        grouped ? (ga.gpb == 2 ? dispatch(qdense_gemm_kernel<kBU8, true, 2>, grid, kThreads, 0, st, ga)
-                               : dispatch(qdense_gemm_kernel<kBU8, true>, grid, kThreads, 0, st, ga))
+        grouped ? dispatch(qdense_gemm_kernel<kBU8, true>, grid, kThreads, 0, st, ga)
                 : dispatch(qdense_gemm_kernel<kBU8, false>, grid, kThreads, 0, st, ga);
         break;
       case MX_DTYPE_INT4:
-        grouped ? (ga.gpb == 2 ? dispatch(qdense_gemm_kernel<kBI4, true, 2>, grid, kThreads, 0, st, ga)
-                               : dispatch(qdense_gemm_kernel<kBI4, true>, grid, kThreads, 0, st, ga))
+        grouped ? dispatch(qdense_gemm_kernel<kBI4, true>, grid, kThreads, 0, st, ga)
                 : dispatch(qdense_gemm_kernel<kBI4, false>, grid, kThreads, 0, st, ga);
         break;
       default:
-        grouped ? (ga.gpb == 2 ? dispatch(qdense_gemm_kernel<kBU4, true, 2>, grid, kThreads, 0, st, ga)
-                               : dispatch(qdense_gemm_kernel<kBU4, true>, grid, kThreads, 0, st, ga))
+        grouped ? dispatch(qdense_gemm_kernel<kBU4, true>, grid, kThreads, 0, st, ga)
                 : dispatch(qdense_gemm_kernel<kBU4, false>, grid, kThreads, 0, st, ga);
         break;
     }
@@ -593,7 +588,8 @@ bool dot_mfma_fits(const DotDesc& d) {
   const bool half = d.in_dt == MX_DTYPE_BFLOAT16 || d.in_dt == MX_DTYPE_FLOAT16;
   return half && (d.out_dt == MX_DTYPE_FLOAT32 || d.out_dt == d.in_dt) && d.M >= 1 && d.K >= kBK && d.K % kBK == 0 && d.N >= 16 &&
          d.N % 16 == 0 && d.B * d.M * d.N * d.K >= ((int64_t)1 << 24) && d.M < (1 << 30) && d.K < (1 << 30) &&
-         d.N < (1 << 30) && aligned(d.lhs, 16) && aligned(d.rhs, 16) && aligned(d.out, 16);
+         d.N < (1 << 30) && d.M * d.K < ((int64_t)1 << 31) && aligned(d.lhs, 16) && aligned(d.rhs, 16) &&
+         aligned(d.out, 16);
 }
 
 int dot_mfma_run(mx_backend* b, const DotDesc& d, const char* name) {
