@@ -60,7 +60,6 @@ constexpr int kXBufs = 3;                            // x buffers: a block's row
 constexpr int kXDma = kABytes / (kWaves * 1024);     // 1 KB direct-to-LDS loads per wave per block
 constexpr int kWLoads = 4;                           // w loads (one per row) per thread per block
 constexpr int kPf = 4;                               // w blocks loaded ahead into registers
-constexpr int kPfGrouped = 2;                        // the same with scale groups
 constexpr int kUnroll = 4;                           // multiple of kPf and of the 2 Bt buffers
 static_assert(kXDma * kWaves * 1024 == kABytes, "x load split");
 static_assert(kBK * kBN == 16 * kThreads, "conversion: 16 weights per thread");
@@ -170,12 +169,9 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
   }
 }
 
-// GPB: blocks per scale group fixed at compile time (1 or 2, folds at fixed steps of the unrolled
-// loop and each group's first MFMAs start from zero), or 0 (read from the arguments).
-template <int BK, bool GRP, int GPB = 0>
+template <int BK, bool GRP>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
-  constexpr int PF = GRP ? kPfGrouped : kPf;
-  static_assert(GPB == 0 || (GRP && kUnroll % GPB == 0), "compile-time groups divide the unroll");
+  constexpr int PF = kPf;
   // With scale groups the tile is 256 x 64: each wave keeps two of the four interleaved MFMA
   // column sets (columns 4*cg + 2*wc + c, c = 0, 1), which halves both accumulator sets so that
   // the second one fits beside the operands without spilling.
@@ -332,7 +328,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[rb][c] = accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // Grouped scales: this lane's 4 columns' scales of the group being summed, loaded a group ahead.
-  // This lane's first column: 64*wc + 4*cg (four consecutive), or 4*cg + 2*wc (two) with groups.
+  // This lane's first column: 64*wc + 4*cg (four consecutive).
   const int lcol = n0 + 64 * wc + 4 * cg;
   const int scol = min(lcol, a.N - NC);
   float sg[NC];
@@ -360,14 +356,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) B[c] = *(const u32x4_v*)(bp + (c ^ b_par) * (kBK * 2));
   };
-  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[NC], auto first) __attribute__((always_inline)) {
+  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[NC]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        if constexpr (GRP && decltype(first)::value)
-          accg[rb][c] = mfma<BK>(A[rb], B[c], f32x4_t{0.f, 0.f, 0.f, 0.f});
-        else if constexpr (GRP)
+        if constexpr (GRP)
           accg[rb][c] = mfma<BK>(A[rb], B[c], accg[rb][c]);
         else
           acc[rb][c] = mfma<BK>(A[rb], B[c], acc[rb][c]);
@@ -381,37 +375,49 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       for (int c = 0; c < NC; ++c) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[rb][c][r] = __builtin_fmaf(accg[rb][c][r], sg[c], acc[rb][c][r]);
-        if constexpr (GPB == 0) accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     load_sg(g + 1);
   };
 
   // x moves by direct-to-LDS loads two blocks ahead of its use (three buffers: block kb's
-  // buffer takes block kb + 3 once its last operands are read, i.e. after block kb's barrier); w
-  // moves through register slots that hold the next PF blocks: block kb's slot is free once
-  // block kb is in LDS (written during block kb - 1), so block kb refills it with block kb + PF
-  // and writes block kb + 1 into the other Bt buffer.  The order keeps the matrix cores fed
-  // while LDS traffic is in flight: on entry step 0's operands of block kb are in registers (A0,
-  // B0); step 1's reads and block kb + 1's Bt writes are issued before step 0's MFMAs, and after
-  // the barrier that publishes block kb + 1 (its Bt writes and its x, whose loads this wave
-  // waits for first), its step-0 reads are issued before step 1's MFMAs.  Every step issues its
-  // loads in one order (w, then x), so the number of loads issued after a block's x loads is
-  // fixed: kWGl + kXDma when that block is published.  (sched_barrier keeps the compiler from
-  // regrouping the phases.)
+  // buffer takes block kb + 3 once its last operands are read, i.e. after block kb's barrier).
+  // w moves through register slots that hold the next PF blocks (slot b % PF holds block b from
+  // its load during block b - PF to its conversion during block b - 2) and is converted into the
+  // Bt buffer that block kb leaves after its barrier (Bt buffers alternate, block b in buffer
+  // b % 2).  Step 0 of block kb reads step 1's operands under its MFMAs; then each wave waits for
+  // its own x loads of block kb + 1 and the barrier publishes that block (x and Bt) and retires
+  // the reads of block kb.  Step 1 reads block kb + 1's step-0 operands, converts and writes block
+  // kb + 2's weights, and issues the loads of blocks kb + PF (w) and kb + 3 (x), all under its
+  // MFMAs.  Every step issues its loads in one order (w, then x), so the number of loads issued
+  // after a block's x loads is fixed: kWGl + kXDma when that block is published.  The weights'
+  // conversion waits for loads two blocks old, and the compiler's count of them (it does not see
+  // the x loads) only adds x loads at least as old as the ones the barrier needs.
+  // (sched_barrier keeps the compiler from regrouping the phases.)
   constexpr int kWGl = kNKB<BK> ? kNKLoads : kWLoads;
-  static_assert(PF >= 2, "the prologue issues two blocks of w loads around the x loads");
+  static_assert(PF >= 3 && kUnroll % PF == 0, "a block's weights are converted two blocks after their load");
   uint32_t wr4[PF][kWWords];
   u32x4_v A0[4], B0[NC], A1[4], B1[NC];
+  int g_left = a.gpb, g_idx = 0;  // scale groups: blocks left in the current group, its index
   auto block = [&](int kb, auto step) __attribute__((always_inline)) {
     constexpr int U = decltype(step)::value;  // kb % kUnroll
-    constexpr int S = U % PF, S1 = (U + 1) % PF, B = U % 2;
+    constexpr int S = U % PF, S2 = (U + 2) % PF, B = U % 2;
     const int xb = (int)((unsigned)kb % kXBufs), xb1 = xb == kXBufs - 1 ? 0 : xb + 1;
-    // Step 0: its MFMAs interleaved with step 1's operand reads, then with the conversion and
-    // LDS writes of block kb + 1, so that every issue stall of a memory instruction overlaps an
-    // MFMA in flight.
     read_step(xb, B, 1, A1, B1);
-    store_w(wr4[S1], B ^ 1);
-    mma_step(A0, B0, std::integral_constant<bool, GPB != 0 && U % (GPB ? GPB : 1) == 0>{});
+    mma_step(A0, B0);
+#pragma unroll
+    for (int i = 0; i < 4 + NC; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm<kWGl + kXDma>();  // this wave's x loads of block kb + 1 are in LDS
+    lds_barrier();
+    read_step(xb1, B ^ 1, 0, A0, B0);
+    store_w(wr4[S2], B);
+    load_w(kb + PF, wr4[S]);
+    dma_x(kb + kXBufs);
+    mma_step(A1, B1);
 #pragma unroll
     for (int i = 0; i < 4 + NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
@@ -423,45 +429,31 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vm<kWGl + kXDma>();  // this wave's x loads of block kb + 1 are in LDS
-    lds_barrier();
-    // Step 1: its MFMAs interleaved with block kb + 1's step-0 reads and the loads of block
-    // kb + PF (w) and kb + 3 (x).
-    read_step(xb1, B ^ 1, 0, A0, B0);
-    load_w(kb + PF, wr4[S]);
-    dma_x(kb + kXBufs);
-    mma_step(A1, B1, std::false_type{});
-#pragma unroll
-    for (int i = 0; i < 4 + NC; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    }
 #pragma unroll
     for (int i = 0; i < kWGl; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (GRP && GPB != 0) {
-      if constexpr ((U + 1) % (GPB ? GPB : 1) == 0) fold(kb / GPB);
-    } else if constexpr (GRP) {
-      if ((kb + 1) % a.gpb == 0) fold(kb / a.gpb);
+    if constexpr (GRP) {
+      if (--g_left == 0) {
+        g_left = a.gpb;
+        fold(g_idx++);
+      }
     }
   };
   auto blocks = [&](int kb, int n, auto... steps) { ((steps.value < n ? block(kb + steps.value, steps) : void()), ...); };
 
-  // Prologue: the loads of blocks 0..2 (x) and 0..PF-1 (w) in the steady state's order (each x
-  // block after one block of w loads), then all of them waited for.
+  // Prologue: the loads of blocks 0..PF-1 (w) and 0..2 (x), all waited for; blocks 0 and 1's
+  // weights into their Bt buffers.
 #pragma unroll
-  for (int p = 0; p + 2 < PF; ++p) load_w(p, wr4[p]);
+  for (int p = 0; p < PF; ++p) load_w(p, wr4[p]);
   dma_x(0);
-  load_w(PF - 2, wr4[PF - 2]);
   dma_x(1);
-  load_w(PF - 1, wr4[PF - 1]);
   dma_x(2);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   store_w(wr4[0], 0);
+  store_w(wr4[1], 1);
   lds_barrier();
   read_step(0, 0, 0, A0, B0);
   int kb = 0;
