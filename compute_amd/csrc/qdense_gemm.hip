@@ -7,9 +7,10 @@
 // The reference's terms (x*w)*s factor per scale group:
 //   y[m,n] = act(bias[n] + sum_g s[g,n] * sum_{k in g} x[m,k]*w[k,n]),
 // with one group for per-channel scales; every product x*w is exact in f32 (bf16 x, |w| < 256),
-// so only the summation order differs from the reference.  With groups, the MFMAs of a group
-// accumulate into a second set of registers that is folded into the total with the group's
-// scales (acc += accg * s[g]) at the group's last block.
+// so only the summation order differs from the reference.  With groups, the MFMAs accumulate
+// into a second set of registers that is folded into the total with the group's scales
+// (acc += accg * s[g]): with bf16 scales after every 64-row block (its first MFMAs start from
+// zero, so nothing is cleared), with f32 scales at the group's last block.
 //
 // Tiling.  A workgroup (8 waves, two per SIMD) computes a 256 x 128 output tile; wave w owns
 // rows [64 wr, 64 wr + 64) x columns [64 wc, 64 wc + 64) with wr = w % 4, wc = w / 4.  K advances
@@ -169,7 +170,11 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
   }
 }
 
-template <int BK, bool GRP>
+// FB (scale groups with bf16 scales): every block's MFMA sums start from zero (C operand 0) and
+// are folded into the total with the scales of the block's group at the block's end, so there is
+// no clearing and no per-block branch (a group of G = 64 j rows is folded j times, once per
+// block).  Otherwise groups are counted at run time and the sums cleared after each fold.
+template <int BK, bool GRP, bool FB = false>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   constexpr int PF = kPf;
   // With scale groups the tile is 256 x 64: each wave keeps two of the four interleaved MFMA
@@ -332,12 +337,19 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   const int lcol = n0 + 64 * wc + 4 * cg;
   const int scol = min(lcol, a.N - NC);
   float sg[NC];
+  u32x2_v sgw = {0u, 0u};
 #pragma unroll
   for (int c = 0; c < NC; ++c) sg[c] = 0.f;
   auto load_sg = [&](int g) __attribute__((always_inline)) {
     g = min(g, a.K / (kBK * max(a.gpb, 1)) - 1);
+    if constexpr (FB) {
+      // bf16 scales (the host takes these kernels for bf16 scales only): one 8-byte load, kept
+      // as loaded until the fold.
+      sgw = *(const u32x2_v*)((const uint16_t*)a.scale + (size_t)g * N + scol);
+    } else {
 #pragma unroll
-    for (int c = 0; c < NC; ++c) sg[c] = load_f(a.scale, (size_t)g * N + scol + c, a.s_dt);
+      for (int c = 0; c < NC; ++c) sg[c] = load_f(a.scale, (size_t)g * N + scol + c, a.s_dt);
+    }
   };
   if constexpr (GRP) load_sg(0);
 
@@ -356,28 +368,37 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) B[c] = *(const u32x4_v*)(bp + (c ^ b_par) * (kBK * 2));
   };
-  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[NC]) __attribute__((always_inline)) {
+  auto mma_step = [&](const u32x4_v (&A)[4], const u32x4_v (&B)[NC], auto fresh) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        if constexpr (GRP)
+        if constexpr (GRP && decltype(fresh)::value)
+          accg[rb][c] = mfma<BK>(A[rb], B[c], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        else if constexpr (GRP)
           accg[rb][c] = mfma<BK>(A[rb], B[c], accg[rb][c]);
         else
           acc[rb][c] = mfma<BK>(A[rb], B[c], acc[rb][c]);
       }
   };
-  // End of scale group g: acc += accg * s[g] (column c of the lane), accg = 0, next group's scales.
-  auto fold = [&](int g) __attribute__((always_inline)) {
+  // End of a scale group (every block with FB): acc += accg * s (this lane's columns; accg = 0
+  // unless the next group's first MFMAs start from zero), then the scales of group g_next.
+  auto fold = [&](int g_next) __attribute__((always_inline)) {
+    if constexpr (FB) {
+      sg[0] = __uint_as_float(sgw[0] << 16);
+      sg[1] = __uint_as_float(sgw[0] & 0xFFFF0000u);
+      sg[2] = __uint_as_float(sgw[1] << 16);
+      sg[3] = __uint_as_float(sgw[1] & 0xFFFF0000u);
+    }
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[rb][c][r] = __builtin_fmaf(accg[rb][c][r], sg[c], acc[rb][c][r]);
-        accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if constexpr (!FB) accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
-    load_sg(g + 1);
+    load_sg(g_next);
   };
 
   // x moves by direct-to-LDS loads two blocks ahead of its use (three buffers: block kb's
@@ -403,8 +424,11 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     constexpr int U = decltype(step)::value;  // kb % kUnroll
     constexpr int S = U % PF, S2 = (U + 2) % PF, B = U % 2;
     const int xb = (int)((unsigned)kb % kXBufs), xb1 = xb == kXBufs - 1 ? 0 : xb + 1;
+    // FB: the block's first step starts its sums from zero (the C operand 0).
+    using Fresh = std::integral_constant<bool, FB>;
+    using Acc = std::integral_constant<bool, false>;
     read_step(xb, B, 1, A1, B1);
-    mma_step(A0, B0);
+    mma_step(A0, B0, Fresh{});
 #pragma unroll
     for (int i = 0; i < 4 + NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
@@ -417,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     store_w(wr4[S2], B);
     load_w(kb + PF, wr4[S]);
     dma_x(kb + kXBufs);
-    mma_step(A1, B1);
+    mma_step(A1, B1, Acc{});
 #pragma unroll
     for (int i = 0; i < 4 + NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
@@ -435,10 +459,18 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (GRP) {
+    if constexpr (GRP && FB) {
+      // Every block's sums are folded with its group's scales; the scale row of the next block
+      // advances every a.gpb blocks (scalar countdown, no branch).
+      const int last = --g_left == 0;
+      g_left = last ? a.gpb : g_left;
+      g_idx += last;
+      fold(g_idx);
+      __builtin_amdgcn_sched_barrier(0);
+    } else if constexpr (GRP) {
       if (--g_left == 0) {
         g_left = a.gpb;
-        fold(g_idx++);
+        fold(++g_idx);
       }
     }
   };
@@ -549,22 +581,30 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.gpb = grouped ? (int)(d.block_size / kBK) : 0;
   const int grid = (int)(tiles_m * tiles_n);
   hipStream_t st = b->stream;
+  // bf16 group scales: the fold-every-block kernel; f32 group scales count blocks at run time.
+  auto grouped_kernel = [&](auto kind) {
+    constexpr int BK = decltype(kind)::value;
+    if (d.s_dt == MX_DTYPE_BFLOAT16)
+      dispatch(qdense_gemm_kernel<BK, true, true>, grid, kThreads, 0, st, ga);
+    else
+      dispatch(qdense_gemm_kernel<BK, true>, grid, kThreads, 0, st, ga);
+  };
   return launch(b, name, [&] {
     switch (d.w_dt) {
       case MX_DTYPE_INT8:
-        grouped ? dispatch(qdense_gemm_kernel<kBI8, true>, grid, kThreads, 0, st, ga)
+        grouped ? grouped_kernel(std::integral_constant<int, kBI8>{})
                 : dispatch(qdense_gemm_kernel<kBI8, false>, grid, kThreads, 0, st, ga);
         break;
       case MX_DTYPE_UINT8:
-        grouped ? dispatch(qdense_gemm_kernel<kBU8, true>, grid, kThreads, 0, st, ga)
+        grouped ? grouped_kernel(std::integral_constant<int, kBU8>{})
                 : dispatch(qdense_gemm_kernel<kBU8, false>, grid, kThreads, 0, st, ga);
         break;
       case MX_DTYPE_INT4:
-        grouped ? dispatch(qdense_gemm_kernel<kBI4, true>, grid, kThreads, 0, st, ga)
+        grouped ? grouped_kernel(std::integral_constant<int, kBI4>{})
                 : dispatch(qdense_gemm_kernel<kBI4, false>, grid, kThreads, 0, st, ga);
         break;
       default:
-        grouped ? dispatch(qdense_gemm_kernel<kBU4, true>, grid, kThreads, 0, st, ga)
+        grouped ? grouped_kernel(std::integral_constant<int, kBU4>{})
                 : dispatch(qdense_gemm_kernel<kBU4, false>, grid, kThreads, 0, st, ga);
         break;
     }
