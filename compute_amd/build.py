@@ -29,8 +29,10 @@ SOURCES = ["runtime.cpp", "graph.cpp", "qdense.hip", "qdense_skinny.hip", "qdens
 
 
 # The skinny kernel takes one arrival ticket per workgroup from a single lane; LLVM's atomic
-# optimizer would turn that atomic into a wave-wide one whose result is waited for at once.
-EXTRA = {"qdense_skinny.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
+# optimizer would turn that atomic into a wave-wide one whose result is waited for at once.  Its
+# leading scalar arguments are preloaded into SGPRs at wave launch.
+EXTRA = {"qdense_skinny.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
+                               "-mllvm", "-amdgpu-kernarg-preload-count=8"]}
 
 
 def _compile(src: str) -> Path:
