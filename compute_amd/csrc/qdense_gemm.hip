@@ -62,6 +62,7 @@ constexpr int kXDma = kABytes / (kWaves * 1024);     // 1 KB direct-to-LDS loads
 constexpr int kWLoads = 4;                           // w loads (one per row) per thread per block
 constexpr int kPf = 4;                               // w blocks loaded ahead into registers
 constexpr int kUnroll = 4;                           // multiple of kPf and of the 2 Bt buffers
+constexpr int64_t kSplitPlanCUs = 256;               // CUs the split tail is planned for (MI355X)
 static_assert(kXDma * kWaves * 1024 == kABytes, "x load split");
 static_assert(kBK * kBN == 16 * kThreads, "conversion: 16 weights per thread");
 
@@ -81,6 +82,14 @@ struct GemmArgs {
   void* out;          // [M, N] bf16 (quantized) or [batch][M, N] f32 / bf16 / f16 (DotGeneral)
   int M, K, N, s_dt, b_dt, act, tiles_n, grouped, tiles, out_dt;
   int gpb;            // blocks of 64 K rows per scale group (grouped scales; scale is [K/G, N])
+  // Split tail (quantized kernels): work items [0, split_from) are whole tiles; the last
+  // (gridDim.x - split_from) / 2 tiles are computed as two halves of K each, by consecutive
+  // workgroups, which exchange f32 partial tiles through `part` (scratch) and count arrivals in
+  // `ctr` (zero between launches); the second to arrive adds the halves (half 0 + half 1) and
+  // stores the tile.  split_from == gridDim.x: no split.
+  int split_from;
+  float* part;        // [tail tiles][2 halves][16][512 threads][4] f32
+  uint32_t* ctr;      // [tail tiles]
 };
 
 template <int BK>
@@ -186,9 +195,15 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // Tile order: consecutive work items go to one XCD (workgroups are dispatched round-robin over
   // the 8); with whole 2 x 16 tile groups, 32 consecutive items form one group.  DotGeneral
   // batches are consecutive runs of items.
-  const int total = gridDim.x;
   const int bid = blockIdx.x;
-  int item = (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
+  const int whole = a.split_from;  // whole-tile work items (dispatched first)
+  int item, half = -1;
+  if (bid < whole) {
+    item = (whole & 7) == 0 ? (bid & 7) * (whole >> 3) + (bid >> 3) : bid;
+  } else {
+    item = whole + ((bid - whole) >> 1);
+    half = (bid - whole) & 1;
+  }
   const int batch = item / a.tiles;
   item -= batch * a.tiles;
   if constexpr (kDotB<BK>) {
@@ -209,8 +224,20 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wr = wave & 3, wc = wave >> 2;
   const int cg = lane & 15, kq = lane >> 4;
-  const int KB = a.K / kBK;
   const size_t N = (size_t)a.N;
+  const int lda = a.K;  // x row stride
+  if constexpr (!kDotB<BK>) {
+    if (half >= 0) {
+      // This workgroup's half of K: the operands start at its first 64-row block (a whole
+      // number of scale groups, checked by the host) and K is the half's extent.
+      const int kbeg = half * (a.K / kBK / 2);
+      a.x += (size_t)kbeg * kBK;
+      a.w += k4B<BK> ? (size_t)kbeg * kBK * N / 2 : (size_t)kbeg * kBK * N;
+      if (a.gpb > 0) a.scale = (const char*)a.scale + (size_t)(kbeg / a.gpb) * N * (a.s_dt == MX_DTYPE_FLOAT32 ? 4 : 2);
+      a.K /= 2;
+    }
+  }
+  const int KB = a.K / kBK;
 
   __shared__ __attribute__((aligned(16))) uint8_t xs[kXBufs][kABytes];
   __shared__ __attribute__((aligned(16))) uint8_t bt[2][kBtBytes];
@@ -224,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < kXDma; ++i) {
     const int r = 8 * (kXDma * wave + i) + (lane >> 3);
-    xoff[i] = 2u * ((uint32_t)min(m0 + r, a.M - 1) * (uint32_t)a.K + 8u * ((lane & 7) ^ ((r >> 1) & 7)));
+    xoff[i] = 2u * ((uint32_t)min(m0 + r, a.M - 1) * (uint32_t)lda + 8u * ((lane & 7) ^ ((r >> 1) & 7)));
   }
   const uint32_t xs_lds = lds_addr(&xs[0][0]) + (uint32_t)(kXDma * wave) * 1024u;
   auto dma_x = [&](int kb) {
@@ -497,6 +524,44 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   for (; kb + kUnroll <= KB; kb += kUnroll) blocks(kb, kUnroll, I0{}, I1{}, I2{}, I3{});
   blocks(kb, KB - kb, I0{}, I1{}, I2{});
 
+  if constexpr (!kDotB<BK>) {
+    if (half >= 0) {
+      // Split tail: store this half's sums, count the arrival; the second to arrive adds the
+      // other half's sums in the order half 0 + half 1 and goes on to the epilogue.  The partial
+      // tiles are stored and loaded with the agent-scope coherence bit (sc1); the two halves run
+      // on different XCDs.
+      __shared__ int s_last;
+      const int tt = item - whole;  // tail tile
+      const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+          a.part + (size_t)tt * 2 * 16 * kThreads * 4, (short)0, 2 * 16 * kThreads * 16, 0x00020000);
+      constexpr int kSc1 = 16;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_v, acc[rb][c]), prs,
+                                                (unsigned)(((half * 16 + 4 * rb + c) * kThreads + t) * 16), 0, kSc1);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (t == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&a.ctr[tt], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == 1u) __hip_atomic_store(&a.ctr[tt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == 1u;
+      }
+      __syncthreads();
+      if (!s_last) return;
+      const int other = half ^ 1;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const f32x4_t o = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            prs, (unsigned)(((other * 16 + 4 * rb + c) * kThreads + t) * 16), 0, kSc1));
+          acc[rb][c] = half == 0 ? acc[rb][c] + o : o + acc[rb][c];
+        }
+    }
+  }
+
   // Epilogue: y = act(acc * s[n] + bias[n]) for this lane's 4 columns (DotGeneral: the f32 sums,
   // or the sums rounded to the half output dtype as ConvertDType rounds them, 4 columns per store).
   const int ncol = lcol;
@@ -579,7 +644,25 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.grouped = (tiles_m % 2 == 0 && tiles_n % 16 == 0) ? 1 : 0;
   ga.tiles = (int)(tiles_m * tiles_n);
   ga.gpb = grouped ? (int)(d.block_size / kBK) : 0;
-  const int grid = (int)(tiles_m * tiles_n);
+  // Split tail: when the tiles leave a last partial round of at most half the CUs (planned for
+  // MI355X's 256 CUs whatever the device reports, so the summation order depends on the shape
+  // only), those tiles are computed as two halves of K by twice as many workgroups.  Not under
+  // mx_qdense_noalloc (its static scratch is smaller than the partial tiles).
+  const int64_t tiles = tiles_m * tiles_n, tail = tiles % kSplitPlanCUs;
+  const int64_t KB = d.K / kBK;
+  const bool split = tiles > kSplitPlanCUs && tail > 0 && 2 * tail <= kSplitPlanCUs && KB % 2 == 0 && KB >= 8 &&
+                     (!grouped || (KB / 2) % ga.gpb == 0) && !b->noalloc_active;
+  ga.split_from = (int)(split ? tiles - tail : tiles);
+  ga.part = nullptr;
+  ga.ctr = nullptr;
+  if (split) {
+    const size_t counter_bytes = 64 * 1024;  // shared with the decode kernels' counters (zero between launches)
+    void* scratch = nullptr;
+    MX_TRY(ensure_scratch(b, counter_bytes + (size_t)tail * 2 * 16 * kThreads * 16, &scratch));
+    ga.ctr = (uint32_t*)scratch;
+    ga.part = (float*)((char*)scratch + counter_bytes);
+  }
+  const int grid = (int)(split ? tiles + tail : tiles);
   hipStream_t st = b->stream;
   // bf16 group scales: the fold-every-block kernel; f32 group scales count blocks at run time.
   auto grouped_kernel = [&](auto kind) {
@@ -640,6 +723,7 @@ int dot_mfma_run(mx_backend* b, const DotDesc& d, const char* name) {
   ga.grouped = (tiles_m % 2 == 0 && tiles_n % 16 == 0) ? 1 : 0;
   ga.tiles = (int)(tiles_m * tiles_n);
   const int grid = (int)(d.B * tiles_m * tiles_n);
+  ga.split_from = grid;  // DotGeneral: whole tiles only
   hipStream_t st = b->stream;
   const bool f16 = d.in_dt == MX_DTYPE_FLOAT16;
   return launch(b, name, [&] {

@@ -120,3 +120,22 @@ def test_gemm_grouped_prefill_full_size(backend, w_dtype, G):
     rows = np.sort(np.random.default_rng(5).choice(p.M, 128, replace=False))
     y = check_rows(r, rows=rows, threads=8, what=f"{w_dtype} g{G}")
     assert np.array_equal(y, r.run())
+
+
+@pytest.mark.parametrize("w_dtype,G,s_dtype,act", [(O.DT_INT8, None, O.DT_FLOAT32, O.ACT_GELU),
+                                                    (O.DT_INT4, 128, O.DT_FLOAT32, O.ACT_NONE),
+                                                    (O.DT_UINT4, 64, O.DT_BFLOAT16, O.ACT_SILU)])
+def test_gemm_split_tail(backend, w_dtype, G, s_dtype, act):
+    """272 tiles of 256 x 128 (x [512, 1024], N = 17408): the 16 tiles past the last whole round of
+    256 are computed as two halves of K whose partial tiles the second half adds (per-channel
+    scales with bias and GELU, f32 and bf16 group scales).  All rows of a sample against the
+    oracle, including the tail tiles' columns; two calls bit-equal (the halves' arrival counters
+    are back at zero)."""
+    M, K, N = 512, 1024, 17408
+    p = O.make_problem(M, K, N, w_dtype=w_dtype, block_axis=0, block_size=G if G else K, per_channel_1d=G is None,
+                       scale_dtype=s_dtype, bias=True, act=act, scale_range=(0.002, 0.02), seed=11 + (G or 0))
+    r = QDenseRun(backend, p)
+    assert r.plan().startswith("qdense_gemm_mfma")
+    rows = np.sort(np.concatenate([np.arange(0, 8), np.arange(256, 264), np.arange(504, 512)]))
+    y = check_rows(r, rows=rows, threads=8, what=f"{w_dtype} G={G}")
+    assert np.array_equal(y, r.run())
