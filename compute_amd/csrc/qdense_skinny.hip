@@ -106,24 +106,21 @@ __device__ __forceinline__ int sk_xcd_swizzle(int bid, int total) {
   return (bid & 7) * (total >> 3) + (bid >> 3);
 }
 
-// Element idx of a bf16 or f32 array p (null: 0), read as the aligned 32-bit word holding it,
-// so that the load is one unconditional instruction whatever the type (the word never leaves the
-// page of the element).  sk_word issues the load, sk_value picks the element once it has arrived.
-struct SkWord {
-  uint32_t w;
-  uint32_t shift;  // moves a bf16 element into the high half: 16 for the low half, else 0
-};
-
-__device__ __forceinline__ SkWord sk_word(const void* p, size_t idx, int dt, const void* dummy) {
-  const bool bf = dt == MX_DTYPE_BFLOAT16;
-  const char* e = p ? (const char*)p + idx * (bf ? 2 : 4) : (const char*)dummy;
-  const uint32_t mis = (uint32_t)(uintptr_t)e & 3u;
-  return SkWord{*(const uint32_t*)(e - mis), bf ? 16u - 8u * (mis & 2u) : 0u};
+// Elements idx .. idx + 3 of a bf16 or f32 array (idx % 4 == 0, the array 16-byte aligned: one
+// 8- or 16-byte load), issued by sk_quad_load and converted once arrived by sk_quad_value.
+__device__ __forceinline__ u32x4_v sk_quad_load(const void* p, size_t idx, int dt) {
+  if (dt == MX_DTYPE_BFLOAT16) {
+    const u32x2_v v = *(const u32x2_v*)((const uint16_t*)p + idx);
+    return u32x4_v{v[0], v[1], 0u, 0u};
+  }
+  return *(const u32x4_v*)((const float*)p + idx);
 }
 
-__device__ __forceinline__ float sk_value(SkWord v, const void* p, int dt) {
-  if (!p) return 0.0f;
-  return dt == MX_DTYPE_BFLOAT16 ? __uint_as_float((v.w << v.shift) & 0xFFFF0000u) : __uint_as_float(v.w);
+__device__ __forceinline__ f32x4_t sk_quad_value(const u32x4_v& w, int dt) {
+  if (dt == MX_DTYPE_BFLOAT16)
+    return f32x4_t{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xFFFF0000u), __uint_as_float(w[1] << 16),
+                   __uint_as_float(w[1] & 0xFFFF0000u)};
+  return __builtin_bit_cast(f32x4_t, w);
 }
 
 // WDT: weight dtype.  MR: rows of the MFMA result kept per lane (1 when M == 1, else 4).
@@ -465,9 +462,10 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
   // The outputs of the column block: the sum of the waves' tiles (one work item) or of the
   // partial tiles in slice order per matrix (each matrix's first tile taken as it is), then bias,
   // activation, bf16, and the folded elementwise op or the pair product, each rounded as the
-  // separate ops round it, and one 8-byte store per quad.  The partial tiles are requested first
-  // and the epilogue operands only when they exist, so that their latencies overlap; the plain
-  // case (bias at most) takes a short path of its own, so that the activation code is not fetched.
+  // separate ops round it, and one 8-byte store per quad.  The epilogue operands (bias, the pair's
+  // second bias, the elementwise operand) are requested first, one vector load each, and the
+  // partial tiles after them, so that all their latencies overlap; the plain case (bias at most)
+  // takes a short path of its own, so that the activation code is not fetched.
   constexpr int kSl = 8;  // partial tiles per batch of loads (all in flight together)
   const bool plain = a.act == MX_ACT_NONE && !a.pair && !a.res_op;
 #pragma unroll 1
@@ -475,6 +473,13 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
     const int g = t + i * kThr;
     const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
     if (g >= NQ || col >= a.N) continue;
+    u32x4_v bq = {0u, 0u, 0u, 0u}, sq = bq;
+    if (a.bias) bq = sk_quad_load(a.bias, col, a.b_dt);
+    if (a.pair) {
+      if (a.bias2) sq = sk_quad_load(a.bias2, col, a.b2_dt);
+    } else if (a.res_op) {
+      sq = sk_quad_load(a.res, (size_t)m * a.N + col, a.res_dt);
+    }
     f32x4_t y, y2;
     if (a.S == 1) {
       // This workgroup holds every tile of the column block.
@@ -500,11 +505,7 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
         }
       }
     }
-    f32x4_t pre = y;
-    if (a.bias) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pre[e] = y[e] + sk_value(sk_word(a.bias, col + e, a.b_dt, a.bias), a.bias, a.b_dt);
-    }
+    const f32x4_t pre = a.bias ? y + sk_quad_value(bq, a.b_dt) : y;
     uint32_t o0, o1;
     if (plain) {
       o0 = (uint32_t)f32_to_bf16(pre[0]) | (uint32_t)f32_to_bf16(pre[1]) << 16;
@@ -513,15 +514,9 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
       // The pair's second pre-activation value, or the elementwise operand.
       f32x4_t sec = y2;
       if (a.pair) {
-        if (a.bias2) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            sec[e] = y2[e] + sk_value(sk_word(a.bias2, col + e, a.b2_dt, a.bias2), a.bias2, a.b2_dt);
-        }
+        if (a.bias2) sec = y2 + sk_quad_value(sq, a.b2_dt);
       } else if (a.res_op) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          sec[e] = sk_value(sk_word(a.res, (size_t)m * a.N + col + e, a.res_dt, a.res), a.res, a.res_dt);
+        sec = sk_quad_value(sq, a.res_dt);
       }
       o0 = 0u;
       o1 = 0u;
@@ -558,8 +553,8 @@ bool qdense_skinny_fits(const QDenseDesc& d) {
          d.block_axis == 0 && d.K >= 32 && d.K % 32 == 0 && G % 32 == 0 && d.N >= 16 &&
          d.N % (dtype_is_packed(d.w_dt) ? 32 : 16) == 0 && d.K < (int64_t)1 << 30 && d.N < (int64_t)1 << 30 &&
          (d.s_dt == MX_DTYPE_BFLOAT16 || d.s_dt == MX_DTYPE_FLOAT32) && aligned(d.w, 16) && aligned(d.x, 16) &&
-         aligned(d.scale, 16) && aligned(d.out, 8) &&
-         (!d.pair || (aligned(d.w2, 16) && aligned(d.scale2, 16) && d.res_op == 0));
+         aligned(d.scale, 16) && aligned(d.out, 8) && aligned(d.bias, 16) && aligned(d.res, 16) &&
+         (!d.pair || (aligned(d.w2, 16) && aligned(d.scale2, 16) && aligned(d.bias2, 16) && d.res_op == 0));
 }
 
 // Steps per wave T: 1 when K/32 is odd; else the smallest even divisor of K/32 whose grid (column
