@@ -132,12 +132,10 @@ __device__ __forceinline__ f32x4_t sk_quad_value(const u32x4_v& w, int dt) {
 // its first step's MFMAs start from zero and its second folds, with no clearing of the sums.
 // WV: waves per workgroup, 8, or 4 for single-row launches whose 8-wave grid would leave a
 // quarter of the CUs idle (twice the workgroups, two per CU).
-// XT (one row of x, T = XT = 4 steps per wave, all of them in one scale group): the wave's 128
-// values of x and its scale row are loaded once, ahead of its first weights, so that a step
-// requests only its weights (C2: 9.71 -> 9.49 us per launch in an A/B on one box).
-// The operands every wave needs first come as separate leading arguments, which the build
-// preloads into SGPRs (-amdgpu-kernarg-preload-count): a wave starts addressing its weights
-// without waiting for a load of its arguments.  The rest stays in SkinnyArgs.
+// XT (T = XT = 4 steps per wave, all of them in one scale group): the wave's scale row is loaded
+// once, ahead of its first weights, and with one row of x (MR == 1) the wave's 128 values of x
+// as well, so that a step requests only its weights (and x for several rows).  C2: 9.71 ->
+// 9.49 us per launch in an A/B on one box.
 template <int WDT, int MR, bool SF32, bool PIPE, bool G2, int WV = kSkWaves, int XT = 0>
 __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_t* px, const uint8_t* pw,
                                                                    const void* pscale, int pK, int pN, int pT,
@@ -210,11 +208,14 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
       const uint16_t* xp = a.x + (size_t)min(cg, a.M - 1) * a.K + 8 * kq;
       const char* sp = (const char*)smat + (size_t)(col0 < a.N ? col0 : 0) * (SF32 ? 4 : 2);
       const size_t srow = (size_t)a.N * (SF32 ? 4 : 2);
-      static_assert(XT == 0 || (XT == 4 && MR == 1 && PIPE && !G2), "XT: one row, four steps per wave");
-      u32x4_v xw[XT ? XT : 1], sw[XT ? kSLoads : 1];
+      static_assert(XT == 0 || (XT == 4 && PIPE && !G2), "XT: four steps per wave");
+      constexpr bool kXW = XT && MR == 1;  // x once per wave
+      u32x4_v xw[kXW ? XT : 1], sw[XT ? kSLoads : 1];
       if constexpr (XT) {
+        if constexpr (kXW) {
   #pragma unroll
-        for (int q = 0; q < XT; ++q) xw[q] = *(const u32x4_v*)(xp + 32 * (k0 + q));
+          for (int q = 0; q < XT; ++q) xw[q] = *(const u32x4_v*)(xp + 32 * (k0 + q));
+        }
         const char* sg0 = sp + (size_t)(k0 / a.FS) * srow;
   #pragma unroll
         for (int q = 0; q < kSLoads; ++q) sw[q] = *(const u32x4_v*)(sg0 + 16 * q);
@@ -230,7 +231,7 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
       };
       int ig = k0 / a.FS, irem = a.FS - k0 % a.FS;  // group and steps left in it, issue order
       auto issue = [&](Slot& sl, int k) __attribute__((always_inline)) {
-        if constexpr (!XT) sl.x = *(const u32x4_v*)(xp + 32 * k);
+        if constexpr (!kXW) sl.x = *(const u32x4_v*)(xp + 32 * k);
         const uint8_t* wk = wp + (size_t)(32 * k) * row_bytes;
   #pragma unroll
         for (int e = 0; e < 8; ++e) sl.w[e] = __builtin_nontemporal_load((const u32x2_v*)(wk + (size_t)e * row_bytes));
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
   #pragma unroll
       for (int c = 0; c < CPL; ++c) grp[c] = zero;
       // A step: dequantise into MFMA B operands and accumulate the group's partial sums.
-      // xa: the step's x operand (the slot's, or with XT the wave's row loaded at entry).
+      // xa: the step's x operand (the slot's, or with one row and XT the wave's x loaded at entry).
       auto compute = [&](const Slot& sl, const u32x4_v& xa, auto zc) __attribute__((always_inline)) {
         constexpr bool Z = decltype(zc)::value;  // the group's first step: sums start from zero
         if constexpr (kI4) {
@@ -338,7 +339,7 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
       int crem = a.FS - k0 % a.FS;  // steps left in the current group, compute order
       // odd: the parity of t, known at each call site (slot A takes even steps, slot B odd ones).
       auto step = [&](const Slot& sl, int t, auto odd) __attribute__((always_inline)) {
-        const u32x4_v& xa = XT ? xw[XT ? t : 0] : sl.x;
+        const u32x4_v& xa = kXW ? xw[kXW ? t : 0] : sl.x;
         if constexpr (G2) {
           // Even steps open a group, odd steps close it.
           if constexpr (!decltype(odd)::value) {
@@ -587,13 +588,11 @@ static int skinny_waves(const QDenseDesc& d, int64_t nb, int num_cus) {
 
 template <int WDT, int MR, bool SF32, int WV = kSkWaves>
 static void launch_pipe(const SkinnyArgs& ga, int grid, size_t lds, hipStream_t st) {
-  // One row, four steps per wave within one scale group (every wave's first step is a multiple
-  // of 4 and FS % 4 == 0): x and the scales are loaded once per wave.
-  if constexpr (MR == 1 && WV == 4) {
-    if (ga.T == 4 && ga.FS % 4 == 0) {
-      dispatch(qdense_skinny_kernel<WDT, 1, SF32, true, false, 4, 4>, grid, 64 * WV, lds, st, ga.x, ga.w, ga.scale, ga.K, ga.N, ga.T, ga.FS, ga.S, ga);
-      return;
-    }
+  // Four steps per wave within one scale group (every wave's first step is a multiple of 4 and
+  // FS % 4 == 0): the scales (and with one row, x) are loaded once per wave.
+  if (ga.T == 4 && ga.FS % 4 == 0) {
+    dispatch(qdense_skinny_kernel<WDT, MR, SF32, true, false, WV, 4>, grid, 64 * WV, lds, st, ga.x, ga.w, ga.scale, ga.K, ga.N, ga.T, ga.FS, ga.S, ga);
+    return;
   }
   if (ga.T >= 2 && ga.FS == 2)
     dispatch(qdense_skinny_kernel<WDT, MR, SF32, true, true, WV>, grid, 64 * WV, lds, st, ga.x, ga.w, ga.scale, ga.K, ga.N, ga.T, ga.FS, ga.S, ga);
