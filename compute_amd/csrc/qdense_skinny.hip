@@ -230,7 +230,9 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
         u32x4_v s[kSLoads];
       };
       int ig = k0 / a.FS, irem = a.FS - k0 % a.FS;  // group and steps left in it, issue order
-      auto issue = [&](Slot& sl, int k) __attribute__((always_inline)) {
+      // odd: the step's parity, known at each call site.  With two-step groups (G2) only the odd
+      // step, which folds the group, needs the scales.
+      auto issue = [&](Slot& sl, int k, auto odd) __attribute__((always_inline)) {
         if constexpr (!kXW) sl.x = *(const u32x4_v*)(xp + 32 * k);
         const uint8_t* wk = wp + (size_t)(32 * k) * row_bytes;
   #pragma unroll
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
         const char* sg = sp + (size_t)ig * srow;
   #pragma unroll
         for (int q = 0; q < kSLoads; ++q) {
-          if constexpr (!XT) sl.s[q] = *(const u32x4_v*)(sg + 16 * q);
+          if constexpr (!XT && !(G2 && !decltype(odd)::value)) sl.s[q] = *(const u32x4_v*)(sg + 16 * q);
         }
         if (--irem == 0) {
           ++ig;
@@ -360,16 +362,16 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
       if constexpr (XT == 4) {
         // The same two-slot pipeline over exactly four steps, written out (static x indices).
         Slot A, B;
-        issue(A, k0);
-        issue(B, k0 + 1);
+        issue(A, k0, False{});
+        issue(B, k0 + 1, True{});
         __builtin_amdgcn_sched_barrier(0);
         step(A, 0, False{});
         __builtin_amdgcn_sched_barrier(0);
-        issue(A, k0 + 2);
+        issue(A, k0 + 2, False{});
         __builtin_amdgcn_sched_barrier(0);
         step(B, 1, True{});
         __builtin_amdgcn_sched_barrier(0);
-        issue(B, k0 + 3);
+        issue(B, k0 + 3, True{});
         __builtin_amdgcn_sched_barrier(0);
         step(A, 2, False{});
         step(B, 3, True{});
@@ -378,26 +380,26 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
         // wave keeps two steps of loads in flight while it computes.  The last two steps are
         // peeled off the loop so that every loop iteration issues the same loads.
         Slot A, B;
-        issue(A, k0);
-        issue(B, k0 + 1);
+        issue(A, k0, False{});
+        issue(B, k0 + 1, True{});
         __builtin_amdgcn_sched_barrier(0);
         int t = 0;
   #pragma unroll 1
         for (; t < a.T - 2; t += 2) {
           step(A, t, False{});
           __builtin_amdgcn_sched_barrier(0);
-          issue(A, k0 + t + 2);
+          issue(A, k0 + t + 2, False{});
           __builtin_amdgcn_sched_barrier(0);
           step(B, t + 1, True{});
           __builtin_amdgcn_sched_barrier(0);
-          issue(B, k0 + t + 3);
+          issue(B, k0 + t + 3, True{});
           __builtin_amdgcn_sched_barrier(0);
         }
         step(A, t, False{});
         step(B, t + 1, True{});
       } else {
         Slot A;
-        issue(A, k0);
+        issue(A, k0, False{});
         step(A, 0, False{});
       }
     }
