@@ -359,7 +359,7 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
         }
       };
   
-      if constexpr (XT == 4) {
+      if constexpr (XT == 4 && kXW) {
         // The same two-slot pipeline over exactly four steps, written out (static x indices).
         Slot A, B;
         issue(A, k0, False{});
