@@ -411,8 +411,10 @@ int mx_qdense_plan(mx_backend* b, const mx_qdense_args* args, char* buf, size_t 
  * MX_QDENSE_NOALLOC_SCRATCH_BYTES per GPU, set up by mx_backend_new and held until the process
  * ends; a problem whose split-K needs more returns MX_ERR_INVALID before anything is launched.
  * Results are bit-identical to mx_qdense's, except for GGML rows past 20 rows, which mx_qdense
- * dequantises into an f32 copy: they run the decode GEMV once per group of four rows (within the
- * f32 accumulation bound of the reference's sum). Every call on one GPU
+ * dequantises into an f32 copy: they run the decode GEMV once per group of four rows, and for
+ * prefill GEMMs whose last partial round of tiles mx_qdense splits into two K halves (at most 128
+ * tiles past a multiple of 256): those tiles are summed whole here (both within the f32
+ * accumulation bound of the reference's sum). Every call on one GPU
  * shares the array, from any backend; the calls are ordered on the device (each call's stream
  * waits for the previous call's completion event), so calls from several streams or backends run
  * one after another.  Under graph capture that wait cannot be recorded: the caller must keep a

@@ -6,7 +6,8 @@ static per-GPU array, so on the skinny, GEMV, GEMM and fused reference-layout pa
 must be bit-identical to mx_qdense's, and within the oracle bars of those paths (bf16 outputs rel
 1e-2 / abs 1e-3 of the reference's f32 result, f32 outputs the f32 accumulation bound).  GGML rows
 past 20 rows, which mx_qdense dequantises into an f32 copy, take the GEMV once per group of four
-rows on the allocation-free call, within the same bound.  Each case makes two
+rows on the allocation-free call, within the same bound, and a GEMM tail that mx_qdense splits
+into two K halves is computed whole (another summation order for those tiles only).  Each case makes two
 calls in a row, the second on a smaller problem, as a caller reusing the shared array would.
 """
 import ctypes as C
@@ -102,6 +103,31 @@ def test_noalloc_matches_qdense(backend, pair, plan):
             assert_bf16_close(got, want, what=f"{p.M}x{p.K}x{p.N}")
         else:
             assert_f32_accumulation_close(got, p, what=f"{p.M}x{p.K}x{p.N}")
+
+
+def test_noalloc_gemm_split_tail_whole(backend):
+    """272 GEMM tiles (x [512, 1024], N = 17408): mx_qdense splits the 16 tiles past the first 256
+    into two K halves that exchange partial tiles through its scratch; the allocation-free call
+    computes them whole.  Outside those tiles (rows 256..511, columns 15360..17407) the results are
+    bit-identical, inside they are another summation order, and both meet the oracle's bars."""
+    pair = [problem(512, 1024, 17408, 14, w_dtype=O.DT_INT8, block_axis=0, block_size=1024, per_channel_1d=True,
+                    scale_dtype=O.DT_FLOAT32, act=O.ACT_GELU),
+            GEMM[1]]
+    for i, p in enumerate(pair):
+        d = Direct(backend, p)
+        assert backend.QDensePlan(d.args(d.outs[0])) == "qdense_gemm_mfma_i8"
+        ref, got = d.run_both()
+        rows = (np.sort(np.concatenate([np.arange(0, 8), np.arange(256, 264), np.arange(p.M - 8, p.M)]))
+                if i == 0 else np.arange(p.M))
+        want = O.qdense_f32(p, rows=rows, threads=8)
+        assert_bf16_close(got[rows], want, what="noalloc")
+        assert_bf16_close(ref[rows], want, what="mx_qdense")
+        if i == 0:
+            tail = np.zeros(got.shape, bool)
+            tail[256:512, 15360:17408] = True
+            assert np.array_equal(got[~tail], ref[~tail]), "tiles outside the split tail differ"
+        else:
+            assert np.array_equal(got, ref)
 
 
 def test_noalloc_reference_layout_fused(backend):
