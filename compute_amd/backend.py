@@ -711,12 +711,18 @@ class Executable:
         _check(self._lib.mx_exec_execute(self._h, arr, don, n, outs, self._nout))
         return [Buffer(self._backend, C.c_void_p(outs[i])) for i in range(self._nout)]
 
-    def ExecuteLoop(self, input_sets: Sequence[Sequence[Buffer]], iters: int) -> None:
-        """Runs Execute `iters` times over rotating input sets, discarding outputs, in one call
-        into the library (no per-iteration foreign-call overhead)."""
+    def LoopSets(self, input_sets: Sequence[Sequence[Buffer]]):
+        """The input sets of ExecuteLoop marshalled once for the library call (a caller timing the
+        loop prepares them outside its timed region)."""
         flat = [b._h.value for s in input_sets for b in s]
-        arr = (C.c_void_p * max(1, len(flat)))(*flat)
-        _check(self._lib.mx_exec_execute_loop(self._h, arr, len(input_sets), self._nin, int(iters)))
+        return (C.c_void_p * max(1, len(flat)))(*flat), len(input_sets)
+
+    def ExecuteLoop(self, input_sets, iters: int) -> None:
+        """Runs Execute `iters` times over rotating input sets, discarding outputs, in one call
+        into the library (no per-iteration foreign-call overhead).  input_sets: a sequence of input
+        sets, or what LoopSets returned for them."""
+        arr, n = input_sets if isinstance(input_sets, tuple) else self.LoopSets(input_sets)
+        _check(self._lib.mx_exec_execute_loop(self._h, arr, n, self._nin, int(iters)))
 
     def Finalize(self) -> None:
         if self._h is not None:

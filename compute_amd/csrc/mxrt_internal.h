@@ -166,6 +166,9 @@ void dev_free(mx_backend* b, void* p);
 // Ensures scratch has at least `bytes` (zero-filled on growth). Returns the device pointer.
 // Inside mx_qdense_noalloc it returns the device's static array instead and never allocates.
 int ensure_scratch(mx_backend* b, size_t bytes, void** out);
+// Waits for the work queued on a stream: polls it for up to 2 ms (the thread keeps its core and
+// returns as soon as the work is done), then blocks.
+hipError_t wait_stream(hipStream_t st);
 // Looks up this device's static scratch array for mx_qdense_noalloc (once per device) and keeps
 // its address in b->noalloc_scratch; b->device must be current.
 int noalloc_scratch_setup(mx_backend* b);

@@ -5,6 +5,7 @@
 // BufferFromFlatData until Finalize, and Execute never copies inputs back to the host.
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <string>
@@ -239,6 +240,37 @@ int ensure_scratch(mx_backend* b, size_t bytes, void** out) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Host waits.  A blocking wait lets the calling thread sleep until the runtime wakes it, which
+// after a wait of a few tens of microseconds costs about as much again; the waits below poll the
+// stream or event for up to kSpinWaitMs, keeping the thread on its core so it returns (and issues
+// its next launches) as soon as the work is done, then fall back to the blocking wait so that a
+// long wait does not occupy a core.
+// ---------------------------------------------------------------------------------------------
+constexpr double kSpinWaitMs = 2.0;
+
+static double now_ms() {
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+hipError_t wait_stream(hipStream_t st) {
+  const double t0 = now_ms();
+  for (;;) {
+    const hipError_t e = hipStreamQuery(st);
+    if (e != hipErrorNotReady) return e;
+    if (now_ms() - t0 > kSpinWaitMs) return hipStreamSynchronize(st);
+  }
+}
+
+static hipError_t wait_event(hipEvent_t ev) {
+  const double t0 = now_ms();
+  for (;;) {
+    const hipError_t e = hipEventQuery(ev);
+    if (e != hipErrorNotReady) return e;
+    if (now_ms() - t0 > kSpinWaitMs) return hipEventSynchronize(ev);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Timing.
 // ---------------------------------------------------------------------------------------------
 static int get_event(mx_backend* b, hipEvent_t* ev) {
@@ -456,7 +488,7 @@ int mx_backend_synchronize(mx_backend* b) {
   clear_error();
   MX_TRY(check_device(b));
   std::lock_guard<std::recursive_mutex> lk(b->mu);
-  MX_CHECK_HIP(hipStreamSynchronize(b->stream));
+  MX_CHECK_HIP(wait_stream(b->stream));
   return MX_OK;
 }
 
@@ -520,7 +552,7 @@ int mx_backend_region_end(mx_backend* b, double* ms) {
   if (!b->region_open) return set_error(MX_ERR_INVALID, "mx_backend_region_end: no region begun");
   b->region_open = false;
   MX_CHECK_HIP(hipEventRecord(b->region_stop, b->stream));
-  MX_CHECK_HIP(hipEventSynchronize(b->region_stop));
+  MX_CHECK_HIP(wait_event(b->region_stop));
   float f = 0.0f;
   MX_CHECK_HIP(hipEventElapsedTime(&f, b->region_start, b->region_stop));
   *ms = f;
@@ -564,7 +596,7 @@ int mx_buffer_from_flat(mx_backend* b, int device, const void* host, size_t host
   MX_TRY(dev_alloc(b, nb, &d));
   if (nb) {
     hipError_t e = hipMemcpyAsync(d, host, nb, hipMemcpyHostToDevice, b->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(b->stream);
+    if (e == hipSuccess) e = wait_stream(b->stream);
     if (e != hipSuccess) {
       dev_free(b, d);
       return set_error(MX_ERR_HIP, "BufferFromFlatData copy failed: %s", hipGetErrorString(e));
@@ -592,7 +624,7 @@ int mx_buffer_to_flat(mx_buffer* buf, void* host, size_t host_nbytes) {
   if (!host) return set_error(MX_ERR_INVALID, "ToFlatData: host is NULL");
   std::lock_guard<std::recursive_mutex> lk(buf->b->mu);
   MX_CHECK_HIP(hipMemcpyAsync(host, buf->dptr, buf->nbytes, hipMemcpyDeviceToHost, buf->b->stream));
-  MX_CHECK_HIP(hipStreamSynchronize(buf->b->stream));
+  MX_CHECK_HIP(wait_stream(buf->b->stream));
   return MX_OK;
 }
 
