@@ -138,8 +138,9 @@ class MLPWorkload:
 
 @dataclass
 class GGMLWorkload:
-    """FusedQuantizedDense over GGML block rows (not a BASELINE config; the SURVEY's next row):
-    f32 x [M, K], weights [N, bytesPerRow] Uint8 in one of the supported block formats."""
+    """FusedQuantizedDense over GGML block rows (not a BASELINE config; the reference's GGML
+    scheme, quantizeddense_ggml.go): f32 x [M, K], weights [N, bytesPerRow] Uint8 in one of the
+    supported block formats."""
 
     name: str
     M: int
@@ -179,8 +180,8 @@ class GGMLWorkload:
 
 @dataclass
 class DotWorkload:
-    """DotGeneral at the prefill shape (the contraction FusedQuantizedDense lowers onto, SURVEY
-    a12-a14): x [M, K] . w [K, N] in bf16, f32 accumulation, bf16 output."""
+    """DotGeneral at the prefill shape (the contraction FusedQuantizedDense lowers onto,
+    standard_ops.go:339-361): x [M, K] . w [K, N] in bf16, f32 accumulation, bf16 output."""
 
     name: str
     M: int
