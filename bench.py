@@ -15,11 +15,12 @@ R1, the reference's own layout at the C2 shape (f32 x, Int4, scales [4096, 86]; 
 and D1, bf16 DotGeneral at the C4 shape (bf16 MFMA roofline).
 
 `value` is algorithmic bytes per step / wall time per step over K back-to-back steps (host
-launch overhead included).  `roofline` prices the dominant kernel's average duration: where one
-kernel is the whole step, the device time per step of the same timed region (a HIP event pair on
-the backend's stream around the K launches); otherwise HIP events recorded around every launch
-over K more steps (`kernel_us_source` says which; per-launch events add work between kernels and
-read longer, so they are used only to split a multi-kernel step).
+launch overhead included: the wall clock starts as the first Execute is issued and stops when
+the host has seen the last step complete).  `roofline` prices the dominant kernel's average
+duration: where one kernel is the whole step, the device time per step of the same timed region
+(a HIP event pair on the backend's stream around the K launches); otherwise HIP events recorded
+around every launch over K more steps (`kernel_us_source` says which; per-launch events add work
+between kernels and read longer, so they are used only to split a multi-kernel step).
 Weight sets are handed out in one rotation across the warm-up, timed and event-timed loops, so
 no loop starts on a set that is still in the Infinity Cache.  Before the warm-up, every copy is
 read once by a read-only pass (the GPU's first access to freshly uploaded memory walks its page
@@ -104,8 +105,8 @@ def measure(backend, wl, steps: int, warmup: int, rotate_bytes: int = 2 * MALL_B
     exe.ExecuteLoop(rot.take(warmup), warmup)
     backend.Synchronize()
     timed = exe.LoopSets(rot.take(steps))
+    backend.RegionBegin()  # the device-side start event; the wall clock starts with the first Execute
     t0 = time.perf_counter()
-    backend.RegionBegin()
     exe.ExecuteLoop(timed, steps)
     region_ms = backend.RegionEnd()  # waits for the stream: the timed region ends here
     wall = time.perf_counter() - t0
