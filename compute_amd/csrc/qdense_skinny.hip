@@ -38,8 +38,8 @@
 //               operand produces.
 //
 // Work decomposition.  The K steps of a column block are dealt out T at a time to waves, in
-// order; a workgroup of NW = 8 waves (4 for one row when 8-wave workgroups would leave a quarter
-// of the CUs idle) takes NW consecutive wave-chunks (one K slice), so a column block has
+// order; a workgroup of NW = 8 waves (7 or 4 for one row when 8-wave workgroups would leave a
+// quarter of the CUs idle) takes NW consecutive wave-chunks (one K slice), so a column block has
 // S = ceil(K/32 / (T*NW)) slices.  T is chosen per shape (the smallest even
 // divisor of K/32 that keeps the grid within one workgroup per CU).  A wave folds a group's
 // partial sums into its total with the group's scale when the group ends, or at its last step.
@@ -100,10 +100,12 @@ __device__ __forceinline__ uint32_t vgpr_const(uint32_t x) {
 }
 
 // Workgroup index -> work item, so that the S slices of one column block (consecutive items)
-// run on one XCD and share its L2: workgroups are dispatched round-robin over the 8 XCDs.
+// run on one XCD and share its L2: workgroups are dispatched round-robin over the 8 XCDs, and
+// each XCD takes a contiguous run of items (any grid size).
 __device__ __forceinline__ int sk_xcd_swizzle(int bid, int total) {
-  if ((total & 7) != 0) return bid;
-  return (bid & 7) * (total >> 3) + (bid >> 3);
+  // XCD x receives workgroups x, x + 8, ...: total / 8 of them, one more when x < total % 8.
+  const int x = bid & 7, base = total >> 3, rem = total & 7;
+  return x * base + min(x, rem) + (bid >> 3);
 }
 
 // Elements idx .. idx + 3 of a bf16 or f32 array (idx % 4 == 0, the array 16-byte aligned: one
@@ -130,8 +132,8 @@ __device__ __forceinline__ f32x4_t sk_quad_value(const u32x4_v& w, int dt) {
 // line it misses costs a trip to L2 or beyond.
 // G2: the scale groups are two steps (G = 64), so a group is exactly one loop iteration's pair:
 // its first step's MFMAs start from zero and its second folds, with no clearing of the sums.
-// WV: waves per workgroup, 8, or 4 for single-row launches whose 8-wave grid would leave a
-// quarter of the CUs idle (twice the workgroups, two per CU).
+// WV: waves per workgroup, 8, or 7 or 4 for single-row launches whose 8-wave grid would leave a
+// quarter of the CUs idle (7: one workgroup per CU; 4: twice the workgroups, up to two per CU).
 // XT (T = XT = 4 steps per wave, all of them in one scale group): the wave's scale row is loaded
 // once, ahead of its first weights, and with one row of x (MR == 1) the wave's 128 values of x
 // as well, so that a step requests only its weights (and x for several rows).  C2: 9.71 ->
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(64 * WV, 2) void qdense_skinny_kernel(const uint16_
 
   const int M = a.M;
   constexpr int kQPR = kCols / 4;  // quads per tile row
-  constexpr int kMaxQ = kSkMaxRows * kQPR / kThr;  // quads per thread (M = 16)
+  constexpr int kMaxQ = (kSkMaxRows * kQPR + kThr - 1) / kThr;  // quads per thread (M = 16)
   const int t = threadIdx.x;
   const int MC = M * kCols, NQ = M * kQPR;
   auto wave_sum = [&](int g) __attribute__((always_inline)) {
@@ -578,14 +580,24 @@ static int skinny_steps(const QDenseDesc& d, int64_t nb, int num_cus, int waves)
   return (int)best;
 }
 
-// Waves per workgroup: 4 for one row when the 8-wave grid would fill at most three quarters of
-// the CUs (C2: 172 workgroups of 8 waves, 9.7-9.9 us as 344 of 4 against 10.1-10.4 us); 8
-// otherwise (batched shapes measured slower with 4: C3 18.1 -> 20.4 us, the MLP 41.5 -> 50.4 us).
+// Waves per workgroup: for one row when the 8-wave grid would fill at most three quarters of the
+// CUs, 7 where seven waves of four steps (one scale group) give one workgroup per CU on at least
+// three quarters of them (C2: 215 workgroups, at most 28 wave-steps per CU, 9.12 us against
+// 9.25 us as 344 of 4, where 88 CUs took two workgroups), else 4 (C2 as 344 of 4: 9.7-9.9 us
+// against 10.1-10.4 us as 172 of 8); 8 otherwise (batched shapes measured slower with 4: C3
+// 18.1 -> 20.4 us, the MLP 41.5 -> 50.4 us).
 static int skinny_waves(const QDenseDesc& d, int64_t nb, int num_cus) {
   if (d.M != 1) return kSkWaves;
   const int64_t T8 = skinny_steps(d, nb, num_cus, kSkWaves);
   const int64_t S8 = (d.K / 32 / T8 + kSkWaves - 1) / kSkWaves;
-  return 4 * nb * S8 <= 3 * (int64_t)num_cus ? 4 : kSkWaves;
+  if (4 * nb * S8 > 3 * (int64_t)num_cus) return kSkWaves;
+  // Seven waves of four steps in one scale group, one workgroup per CU filling at least three
+  // quarters of them.
+  const int64_t T7 = skinny_steps(d, nb, num_cus, 7);
+  const int64_t S7 = (d.K / 32 / T7 + 6) / 7;
+  const int64_t G = std::min<int64_t>(d.block_size, d.K) / 32;
+  if (T7 == 4 && G % 4 == 0 && nb * S7 <= num_cus && 4 * nb * S7 >= 3 * (int64_t)num_cus) return 7;
+  return 4;
 }
 
 template <int WDT, int MR, bool SF32, int WV = kSkWaves>
@@ -606,7 +618,12 @@ static void launch_pipe(const SkinnyArgs& ga, int grid, size_t lds, hipStream_t 
 
 template <int WDT>
 static void launch_skinny(const SkinnyArgs& ga, bool sf32, int waves, int grid, size_t lds, hipStream_t st) {
-  if (ga.M == 1 && waves == 4) {
+  if (ga.M == 1 && waves == 7) {  // four steps per wave in one scale group (the plan checks)
+    if (sf32)
+      dispatch(qdense_skinny_kernel<WDT, 1, true, true, false, 7, 4>, grid, 64 * 7, lds, st, ga.x, ga.w, ga.scale, ga.K, ga.N, ga.T, ga.FS, ga.S, ga);
+    else
+      dispatch(qdense_skinny_kernel<WDT, 1, false, true, false, 7, 4>, grid, 64 * 7, lds, st, ga.x, ga.w, ga.scale, ga.K, ga.N, ga.T, ga.FS, ga.S, ga);
+  } else if (ga.M == 1 && waves == 4) {
     if (sf32)
       launch_pipe<WDT, 1, true, 4>(ga, grid, lds, st);
     else
