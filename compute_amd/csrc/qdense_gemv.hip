@@ -42,6 +42,8 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float gv_f32x4;
 typedef uint32_t gv_u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGvWaves = 8;
+constexpr int kGvWavesWide = 12;  // one-row launches that would otherwise leave CUs with two workgroups
+constexpr int kGvPlanCUs = 256;   // CUs the split is planned for (MI355X)
 constexpr int kGvThreads = 64 * kGvWaves;
 constexpr int kGvRows = 32;                      // K rows per wave
 constexpr int kGvSlice = kGvRows * kGvWaves;     // K rows per workgroup
@@ -68,8 +70,9 @@ struct GemvArgs {
 };
 
 __device__ __forceinline__ int gv_xcd_swizzle(int bid, int total) {
-  if ((total & 7) != 0) return bid;
-  return (bid & 7) * (total >> 3) + (bid >> 3);
+  // XCD x receives workgroups x, x + 8, ...: total / 8 of them, one more when x < total % 8.
+  const int x = bid & 7, base = total >> 3, rem = total & 7;
+  return x * base + min(x, rem) + (bid >> 3);
 }
 
 // Element idx of a bf16 or f32 array p (null: dummy), read as the aligned 32-bit word holding it
@@ -110,8 +113,9 @@ __device__ __forceinline__ void gv_pin(float (&v)[MR]) {
 // folded into x row by row).  0: blocks of B rows along K, [ceil(K/B), N] (B % 32 == 0 or B >= K,
 // so a wave's 32 rows share one group: the wave sums x*w' and x over its rows and applies its
 // columns' scale and zero point once).
-template <int WK, int MR, int AX>
-__global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
+template <int WK, int MR, int AX, int WV = kGvWaves>
+__global__ __launch_bounds__(64 * WV) void qdense_gemv_kernel(GemvArgs a) {
+  constexpr int kWv = WV, kThr = 64 * WV, kSlice = kGvRows * WV;
   constexpr bool k4 = WK == kGvI4 || WK == kGvU4 || WK == kGvNF4;
   constexpr bool kNF = WK == kGvNF8 || WK == kGvNF4;
   constexpr int CPL = k4 ? 8 : 4;        // columns per lane
@@ -129,7 +133,7 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int cblk = cb * kCols;
   const int col0 = cblk + lane * CPL;
-  const int kw = slice * kGvSlice + wave * kGvRows;  // first K row of this wave
+  const int kw = slice * kSlice + wave * kGvRows;  // first K row of this wave
   const int M = a.M;
   const bool has_zp = a.zp != nullptr;
 
@@ -321,12 +325,12 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
   auto wave_sum = [=](int g) {
     gv_f32x4 y = *(const gv_f32x4*)(red + 4 * g);
 #pragma unroll
-    for (int w = 1; w < kGvWaves; ++w) y += *(const gv_f32x4*)(red + w * MC + 4 * g);
+    for (int w = 1; w < kWv; ++w) y += *(const gv_f32x4*)(red + w * MC + 4 * g);
     return y;
   };
 
   if (a.S == 1) {
-    for (int g = t; g < NQ; g += kGvThreads) finish_quad(g / kQPR, cblk + 4 * (g % kQPR), wave_sum(g));
+    for (int g = t; g < NQ; g += kThr) finish_quad(g / kQPR, cblk + 4 * (g % kQPR), wave_sum(g));
     return;
   }
 
@@ -337,7 +341,7 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
       a.partial, (short)0, (int)((size_t)a.S * M * a.N * sizeof(float)), 0x00020000);
   constexpr int kSc1 = 16;  // cache-policy operand of the buffer intrinsics: sc1
-  for (int g = t; g < NQ; g += kGvThreads) {
+  for (int g = t; g < NQ; g += kThr) {
     const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
     if (col < a.N)
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(gv_u32x4, wave_sum(g)), prs,
@@ -354,7 +358,7 @@ __global__ __launch_bounds__(kGvThreads) void qdense_gemv_kernel(GemvArgs a) {
   __syncthreads();
   if (!s_last) return;
   constexpr int kSl = 16;
-  for (int g = t; g < NQ; g += kGvThreads) {
+  for (int g = t; g < NQ; g += kThr) {
     const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
     const int c = min(col, a.N - 4);
     gv_f32x4 y = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -408,19 +412,21 @@ bool qdense_gemv_fits(const QDenseDesc& d) {
 }
 
 template <int WK, int AX>
-static void gemv_launch_ax(const GemvArgs& ga, int grid, size_t lds, hipStream_t st) {
-  if (ga.M == 1)
+static void gemv_launch_ax(const GemvArgs& ga, int waves, int grid, size_t lds, hipStream_t st) {
+  if (ga.M == 1 && waves == kGvWavesWide)
+    dispatch(qdense_gemv_kernel<WK, 1, AX, kGvWavesWide>, grid, 64 * kGvWavesWide, lds, st, ga);
+  else if (ga.M == 1)
     dispatch(qdense_gemv_kernel<WK, 1, AX>, grid, kGvThreads, lds, st, ga);
   else
     dispatch(qdense_gemv_kernel<WK, kGvMaxRows, AX>, grid, kGvThreads, lds, st, ga);
 }
 
 template <int WK>
-static void gemv_launch(const GemvArgs& ga, int axis, int grid, size_t lds, hipStream_t st) {
+static void gemv_launch(const GemvArgs& ga, int axis, int waves, int grid, size_t lds, hipStream_t st) {
   if (axis == 1)
-    gemv_launch_ax<WK, 1>(ga, grid, lds, st);
+    gemv_launch_ax<WK, 1>(ga, waves, grid, lds, st);
   else
-    gemv_launch_ax<WK, 0>(ga, grid, lds, st);
+    gemv_launch_ax<WK, 0>(ga, waves, grid, lds, st);
 }
 
 static int gemv_run_rows(mx_backend* b, const QDenseDesc& d, const char* name);
@@ -443,7 +449,16 @@ static int gemv_run_rows(mx_backend* b, const QDenseDesc& d, const char* name) {
   const bool packed = dtype_is_packed(d.w_dt);
   const int64_t cols = packed ? 512 : 256;
   const int64_t nb = (d.N + cols - 1) / cols;
-  const int64_t S = (d.K + kGvSlice - 1) / kGvSlice;
+  // One row: twelve-wave workgroups where the 8-wave grid would give some CUs two workgroups and
+  // twelve waves give one workgroup per CU on at least three quarters of them (planned for
+  // MI355X's 256 CUs whatever the device reports, so the split, and the bits, depend on the
+  // shape only).
+  const int64_t S8 = (d.K + kGvSlice - 1) / kGvSlice;
+  const int64_t SW = (d.K + kGvRows * kGvWavesWide - 1) / (kGvRows * kGvWavesWide);
+  const int waves = d.M == 1 && nb * S8 > kGvPlanCUs && nb * SW <= kGvPlanCUs && 4 * nb * SW >= 3 * kGvPlanCUs
+                        ? kGvWavesWide
+                        : kGvWaves;
+  const int64_t S = waves == kGvWaves ? S8 : SW;
   const size_t counter_bytes = 64 * 1024;
   if ((size_t)nb * 4 > counter_bytes || nb * S > (int64_t)1 << 30 || S * d.M * d.N * 4 >= (int64_t)1 << 31)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: N=%lld too large for the GEMV path", (long long)d.N);
@@ -475,19 +490,19 @@ static int gemv_run_rows(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.b_dt = d.b_dt;
   const int mr = d.M == 1 ? 1 : kGvMaxRows;
   const size_t stage =
-      (size_t)kGvWaves * (kGvRows * mr + (d.block_axis == 1 ? 2 * kGvRows * kGvSStride : 0)) * sizeof(float);
-  const size_t tiles = (size_t)kGvWaves * d.M * cols * sizeof(float);
+      (size_t)waves * (kGvRows * mr + (d.block_axis == 1 ? 2 * kGvRows * kGvSStride : 0)) * sizeof(float);
+  const size_t tiles = (size_t)waves * d.M * cols * sizeof(float);
   const size_t lds = std::max(stage, tiles);
   const int grid = (int)(nb * S);
   hipStream_t st = b->stream;
   return launch(b, name, [&] {
     switch (gemv_kind(d)) {
-      case kGvI8: gemv_launch<kGvI8>(ga, d.block_axis, grid, lds, st); break;
-      case kGvU8: gemv_launch<kGvU8>(ga, d.block_axis, grid, lds, st); break;
-      case kGvI4: gemv_launch<kGvI4>(ga, d.block_axis, grid, lds, st); break;
-      case kGvU4: gemv_launch<kGvU4>(ga, d.block_axis, grid, lds, st); break;
-      case kGvNF8: gemv_launch<kGvNF8>(ga, d.block_axis, grid, lds, st); break;
-      default: gemv_launch<kGvNF4>(ga, d.block_axis, grid, lds, st); break;
+      case kGvI8: gemv_launch<kGvI8>(ga, d.block_axis, waves, grid, lds, st); break;
+      case kGvU8: gemv_launch<kGvU8>(ga, d.block_axis, waves, grid, lds, st); break;
+      case kGvI4: gemv_launch<kGvI4>(ga, d.block_axis, waves, grid, lds, st); break;
+      case kGvU4: gemv_launch<kGvU4>(ga, d.block_axis, waves, grid, lds, st); break;
+      case kGvNF8: gemv_launch<kGvNF8>(ga, d.block_axis, waves, grid, lds, st); break;
+      default: gemv_launch<kGvNF4>(ga, d.block_axis, waves, grid, lds, st); break;
     }
   });
 }
