@@ -306,9 +306,13 @@ __global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
       dst[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off < end ? off : 0x7FFFFFF0u, 0, 0);
     }
   };
-  const int64_t stride = (int64_t)gridDim.x * kGvWaves;
-  int64_t n = (int64_t)blockIdx.x * kGvWaves + wave;
-  if (n < d.N) issue(n, pre);  // before staging x: the first row travels meanwhile
+  // Each workgroup takes a contiguous run of rows, N / grid of them (one more for the first
+  // N % grid), so that no CU has more than one row above the average; its waves take every
+  // WV-th row of the run.
+  const int64_t r1 = (int64_t)(blockIdx.x + 1) * d.N / gridDim.x;
+  const int64_t stride = kGvWaves;
+  int64_t n = (int64_t)blockIdx.x * d.N / gridDim.x + wave;
+  if (n < r1) issue(n, pre);  // before staging x: the first row travels meanwhile
   // x staged as [MR][units][kGvPad] floats with 16-byte loads, kGvXB of them issued before their
   // stores (K % 32 == 0, x 16-byte aligned).
   {
@@ -346,10 +350,10 @@ __global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
   }
   __syncthreads();
 
-  for (; n < d.N; n += stride) {
+  for (; n < r1; n += stride) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) *(u32x4_v*)(rb + 16 * (lane + 64 * i)) = pre[i];
-    if (n + stride < d.N) issue(n + stride, pre);
+    if (n + stride < r1) issue(n + stride, pre);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
