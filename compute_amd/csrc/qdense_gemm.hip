@@ -15,15 +15,15 @@
 // Tiling.  A workgroup (8 waves, two per SIMD) computes a 256 x 128 output tile; wave w owns
 // rows [64 wr, 64 wr + 64) x columns [64 wc, 64 wc + 64) with wr = w % 4, wc = w / 4.  K advances
 // in blocks of 64 (two 32-row steps of v_mfma_f32_16x16x32_bf16).  LDS holds
-//   - x, three buffers: [256 rows][64 k] bf16; 16-byte k-chunks XOR-swizzled within each row by
+//   - x, four buffers (three with f32 group scales): [256 rows][64 k] bf16; 16-byte k-chunks XOR-swizzled within each row by
 //     (row >> 1) & 7 so that an MFMA operand read (16 rows) hits distinct banks;
 //   - Bt, two buffers: [128 columns][64 k] bf16, the weights converted exactly to bf16 (|w| < 256
 //     has at most 8 significant bits) and transposed.  Column c is stored in row p = c ^ ((c >> 2)
 //     & 1) and its 16-byte k-chunks are XOR-swizzled by (p >> 3) & 7: the 16 lanes of a B-operand
 //     read (columns 4 apart) then cover both halves of the banks and 8 distinct chunks in each.
 // x moves straight from memory into its LDS buffer (global_load_lds_dwordx4, 1 KB = 8 rows per
-// wave instruction, the swizzle applied by choosing each lane's source chunk) two blocks ahead of
-// its use, and takes no registers, VALU or LDS-write instructions; that leaves room for the
+// wave instruction, the swizzle applied by choosing each lane's source chunk) three blocks ahead of
+// its use (two with f32 group scales), and takes no registers, VALU or LDS-write instructions; that leaves room for the
 // grouped kernels' second accumulator set beside a full 256 x 128 tile.  The weights travel
 // through registers (loads of block kb + PF issued during block kb, each thread 4 rows x 4
 // columns: 4 bytes of int8, 2 of 4-bit or 8 of a half type per row; 32 threads per row segment),
@@ -57,7 +57,12 @@ typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
 constexpr int kBM = 256, kBN = 128, kBK = 64, kWaves = 8, kThreads = 64 * kWaves;
 constexpr int kABytes = kBM * kBK * 2;   // 32 KB per x buffer
 constexpr int kBtBytes = kBN * kBK * 2;  // 16 KB per Bt buffer
-constexpr int kXBufs = 3;                            // x buffers: a block's rows land two blocks ahead
+// x buffers: a block's rows are requested kXBufs - 1 blocks ahead of its use.  Four (160 KB of
+// LDS with the two Bt buffers) except for f32 group scales, whose run-time group branch leaves no
+// registers for the longer wait (three: 128 KB).  Q1 360 -> 351 us, Q2 360 -> 346 us, D1 98 -> 95 us
+// per call with four; C4 unchanged.
+template <int BK, bool GRP, bool FB>
+constexpr int kXBufs = (GRP && !FB) ? 3 : 4;
 constexpr int kXDma = kABytes / (kWaves * 1024);     // 1 KB direct-to-LDS loads per wave per block
 constexpr int kWLoads = 4;                           // w loads (one per row) per thread per block
 constexpr int kPf = 4;                               // w blocks loaded ahead into registers
@@ -138,11 +143,15 @@ __device__ __forceinline__ void lds_dma_b128(const void* base, uint32_t voff, ui
 // Waits until at most N of this wave's memory loads are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vm() {
-  static_assert(N == 6 || N == 8, "counts used by the kernel");
+  static_assert(N == 6 || N == 8 || N == 12 || N == 16, "counts used by the kernel");
   if constexpr (N == 6)
     asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-  else
+  else if constexpr (N == 8)
     asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if constexpr (N == 12)
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
 }
 
 typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
@@ -239,7 +248,8 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   }
   const int KB = a.K / kBK;
 
-  __shared__ __attribute__((aligned(16))) uint8_t xs[kXBufs][kABytes];
+  constexpr int XB = kXBufs<BK, GRP, FB>;
+  __shared__ __attribute__((aligned(16))) uint8_t xs[XB][kABytes];
   __shared__ __attribute__((aligned(16))) uint8_t bt[2][kBtBytes];
 
   // x: each wave moves kXDma 1 KB pieces of a block straight into LDS: piece q = kXDma*wave + i
@@ -255,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   }
   const uint32_t xs_lds = lds_addr(&xs[0][0]) + (uint32_t)(kXDma * wave) * 1024u;
   auto dma_x = [&](int kb) {
-    const uint32_t dst = xs_lds + (uint32_t)(kb % kXBufs) * kABytes;
+    const uint32_t dst = xs_lds + (uint32_t)(kb % XB) * kABytes;
     kb = min(kb, KB - 1);
 #pragma unroll
     for (int i = 0; i < kXDma; ++i) lds_dma_b128(a.x + (size_t)kb * kBK, xoff[i], dst + 1024u * i);
@@ -428,17 +438,17 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     load_sg(g_next);
   };
 
-  // x moves by direct-to-LDS loads two blocks ahead of its use (three buffers: block kb's
-  // buffer takes block kb + 3 once its last operands are read, i.e. after block kb's barrier).
+  // x moves by direct-to-LDS loads XB - 1 blocks ahead of its use (XB buffers: block kb's
+  // buffer takes block kb + XB once its last operands are read, i.e. after block kb's barrier).
   // w moves through register slots that hold the next PF blocks (slot b % PF holds block b from
   // its load during block b - PF to its conversion during block b - 2) and is converted into the
   // Bt buffer that block kb leaves after its barrier (Bt buffers alternate, block b in buffer
   // b % 2).  Step 0 of block kb reads step 1's operands under its MFMAs; then each wave waits for
   // its own x loads of block kb + 1 and the barrier publishes that block (x and Bt) and retires
   // the reads of block kb.  Step 1 reads block kb + 1's step-0 operands, converts and writes block
-  // kb + 2's weights, and issues the loads of blocks kb + PF (w) and kb + 3 (x), all under its
+  // kb + 2's weights, and issues the loads of blocks kb + PF (w) and kb + XB (x), all under its
   // MFMAs.  Every step issues its loads in one order (w, then x), so the number of loads issued
-  // after a block's x loads is fixed: kWGl + kXDma when that block is published.  The weights'
+  // after a block's x loads is fixed: (XB - 2) * (kWGl + kXDma) when that block is published.  The weights'
   // conversion waits for loads two blocks old, and the compiler's count of them (it does not see
   // the x loads) only adds x loads at least as old as the ones the barrier needs.
   // (sched_barrier keeps the compiler from regrouping the phases.)
@@ -450,7 +460,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   auto block = [&](int kb, auto step) __attribute__((always_inline)) {
     constexpr int U = decltype(step)::value;  // kb % kUnroll
     constexpr int S = U % PF, S2 = (U + 2) % PF, B = U % 2;
-    const int xb = (int)((unsigned)kb % kXBufs), xb1 = xb == kXBufs - 1 ? 0 : xb + 1;
+    const int xb = (int)((unsigned)kb % XB), xb1 = xb == XB - 1 ? 0 : xb + 1;
     // FB: the block's first step starts its sums from zero (the C operand 0).
     using Fresh = std::integral_constant<bool, FB>;
     using Acc = std::integral_constant<bool, false>;
@@ -462,12 +472,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
     __builtin_amdgcn_sched_barrier(0);
-    wait_vm<kWGl + kXDma>();  // this wave's x loads of block kb + 1 are in LDS
+    wait_vm<(XB - 2) * (kWGl + kXDma)>();  // this wave's x loads of block kb + 1 are in LDS
     lds_barrier();
     read_step(xb1, B ^ 1, 0, A0, B0);
     store_w(wr4[S2], B);
     load_w(kb + PF, wr4[S]);
-    dma_x(kb + kXBufs);
+    dma_x(kb + XB);
     mma_step(A1, B1, Acc{});
 #pragma unroll
     for (int i = 0; i < 4 + NC; ++i) {
@@ -503,13 +513,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   };
   auto blocks = [&](int kb, int n, auto... steps) { ((steps.value < n ? block(kb + steps.value, steps) : void()), ...); };
 
-  // Prologue: the loads of blocks 0..PF-1 (w) and 0..2 (x), all waited for; blocks 0 and 1's
+  // Prologue: the loads of blocks 0..PF-1 (w) and 0..XB-1 (x), all waited for; blocks 0 and 1's
   // weights into their Bt buffers.
 #pragma unroll
   for (int p = 0; p < PF; ++p) load_w(p, wr4[p]);
-  dma_x(0);
-  dma_x(1);
-  dma_x(2);
+#pragma unroll
+  for (int p = 0; p < XB; ++p) dma_x(p);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   store_w(wr4[0], 0);
   store_w(wr4[1], 1);
@@ -530,7 +539,9 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       // other half's sums in the order half 0 + half 1 and goes on to the epilogue.  The partial
       // tiles are stored and loaded with the agent-scope coherence bit (sc1); the two halves run
       // on different XCDs.
-      __shared__ int s_last;
+      // The arrival flag takes the first word of a Bt buffer: every wave has left the main loop
+      // (the barrier below comes first), and four x buffers leave no LDS beyond the two.
+      int& s_last = *(int*)&bt[0][0];
       const int tt = item - whole;  // tail tile
       const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
           a.part + (size_t)tt * 2 * 16 * kThreads * 4, (short)0, 2 * 16 * kThreads * 16, 0x00020000);
