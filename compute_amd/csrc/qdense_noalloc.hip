@@ -71,17 +71,22 @@ int noalloc_scratch_setup(mx_backend* b) {
     return set_error(MX_ERR_HIP, "hipEventCreate for mx_qdense_noalloc on device %d failed: %s", b->device,
                      hipGetErrorString(ee));
   }
+  // On failure the ordering state is released again (nothing has been published yet).
+  auto fail = [&](const char* what, hipError_t err) {
+    hipEventDestroy(ord->done);
+    delete ord;
+    return set_error(MX_ERR_HIP, "%s for mx_qdense_noalloc on device %d failed: %s", what, b->device,
+                     hipGetErrorString(err));
+  };
   void* ptr = nullptr;
   hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
-  if (e != hipSuccess || ptr == nullptr)
-    return set_error(MX_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", b->device,
-                     hipGetErrorString(e));
+  if (e != hipSuccess || ptr == nullptr) return fail("hipGetSymbolAddress(scratch)", e);
   // The counters start at zero.  The stream is synchronised so that work on any other stream of
   // this device sees the cleared counters.
   const int words = (int)(kCounterBytes / 4);
   hipLaunchKernelGGL(clear_words, dim3((words + 255) / 256), dim3(256), 0, b->stream, (uint32_t*)ptr, words);
-  MX_CHECK_HIP(hipGetLastError());
-  MX_CHECK_HIP(hipStreamSynchronize(b->stream));
+  if ((e = hipGetLastError()) != hipSuccess) return fail("clearing the counters", e);
+  if ((e = hipStreamSynchronize(b->stream)) != hipSuccess) return fail("clearing the counters", e);
   g_scratch_ptr[b->device] = ptr;
   g_order[b->device] = ord;
   b->noalloc_scratch = ptr;
