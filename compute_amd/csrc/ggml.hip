@@ -288,7 +288,10 @@ __global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
   // The weights are read in whole 16-byte units from a 16-byte-aligned base: the buffer's range
   // is its size rounded up to 16 (a partially valid unit must come back whole; the bytes past
   // the end lie in the same allocation granule, 256 bytes or more) and units beyond it read 0.
-  const int64_t total = (d.N * d.bpr + 15) & ~(int64_t)15;
+  // A row (or its K segment: bpr bytes from row_off) starts r * rstride + row_off bytes in.
+  const int64_t rstride = d.row_stride ? d.row_stride : d.bpr;
+  const int64_t ldx = d.ldx ? d.ldx : d.K;
+  const int64_t total = (d.N * rstride + 15) & ~(int64_t)15;
   const __amdgpu_buffer_rsrc_t wrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(d.w), (short)0, (int)total, 0x00020000);
   // A row is loaded into registers one row ahead (16-byte loads from the aligned address at or
@@ -299,7 +302,8 @@ __global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
   u32x4_v pre[CH];
   auto issue = [&](int64_t row, u32x4_v (&dst)[CH]) {
     const int64_t r = min(row, d.N - 1);
-    const uint32_t a0 = (uint32_t)((r * d.bpr) & ~(int64_t)15), end = (uint32_t)(r * d.bpr + d.bpr);
+    const int64_t rs = r * rstride + d.row_off;
+    const uint32_t a0 = (uint32_t)(rs & ~(int64_t)15), end = (uint32_t)(rs + d.bpr);
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const uint32_t off = a0 + 16u * (lane + 64 * i);
@@ -314,20 +318,24 @@ __global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
   int64_t n = (int64_t)blockIdx.x * d.N / gridDim.x + wave;
   if (n < r1) issue(n, pre);  // before staging x: the first row travels meanwhile
   // x staged as [MR][units][kGvPad] floats with 16-byte loads, kGvXB of them issued before their
-  // stores (K % 32 == 0, x 16-byte aligned).
+  // stores (K % 32 == 0, ldx % 4 == 0, x 16-byte aligned).
   {
-    const int q4 = MR * K / 4;
-    for (int base = t; base < q4; base += kGvXB * kGvThreads) {
-      float4 v[kGvXB];
+    const int q4 = K / 4;
 #pragma unroll
-      for (int j = 0; j < kGvXB; ++j)  // unconditional (clamped) so that they stay in registers
-        v[j] = reinterpret_cast<const float4*>(d.x)[min(base + j * kGvThreads, q4 - 1)];
+    for (int m = 0; m < MR; ++m) {
+      const float4* xr = reinterpret_cast<const float4*>(d.x + m * ldx);
+      for (int base = t; base < q4; base += kGvXB * kGvThreads) {
+        float4 v[kGvXB];
 #pragma unroll
-      for (int j = 0; j < kGvXB; ++j) {
-        const int i = base + j * kGvThreads;
-        if (i < q4) {
-          const int m = 4 * i / K, k = 4 * i - m * K;
-          *reinterpret_cast<float4*>(xs + (m * units + (k >> 5)) * kGvPad + (k & 31)) = v[j];
+        for (int j = 0; j < kGvXB; ++j)  // unconditional (clamped) so that they stay in registers
+          v[j] = xr[min(base + j * kGvThreads, q4 - 1)];
+#pragma unroll
+        for (int j = 0; j < kGvXB; ++j) {
+          const int i = base + j * kGvThreads;
+          if (i < q4) {
+            const int k = 4 * i;
+            *reinterpret_cast<float4*>(xs + (m * units + (k >> 5)) * kGvPad + (k & 31)) = v[j];
+          }
         }
       }
     }
@@ -357,7 +365,7 @@ __global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-    const uint8_t* row = rb + (int)((n * d.bpr) & 15);
+    const uint8_t* row = rb + (int)((n * rstride + d.row_off) & 15);
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
@@ -380,8 +388,13 @@ __global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         float v = acc[m];
-        if (d.bias) v = add_rn(v, d.bias[n]);
-        d.out[(size_t)m * d.N + n] = act_ref(v, d.act);
+        float* o = d.out + (size_t)m * d.N + n;
+        if (d.accumulate) v = add_rn(*o, v);  // the earlier K segments' sum first
+        if (d.epilogue) {
+          if (d.bias) v = add_rn(v, d.bias[n]);
+          v = act_ref(v, d.act);
+        }
+        *o = v;
       }
     }
     // Every lane's reads of the row are done before the next row is staged over it.
@@ -394,8 +407,9 @@ __global__ __launch_bounds__(64 * WV) void ggml_gemv_kernel(GgmlDesc d) {
 // Chunks per lane (2, 4 or 8), waves per workgroup (8 or 16) and LDS of the GEMV for these
 // sizes, or 0 if it does not apply.
 static size_t ggml_gemv_lds(const GgmlDesc& d, int* ch, int* waves) {
-  if (d.M < 1 || d.M > 4 || d.K % 32 != 0 || d.K > (1 << 20) || d.N * d.bpr + 16 >= ((int64_t)1 << 31) ||
-      (uintptr_t)d.w % 16 != 0 || (uintptr_t)d.x % 16 != 0)
+  const int64_t rstride = d.row_stride ? d.row_stride : d.bpr, ldx = d.ldx ? d.ldx : d.K;
+  if (d.M < 1 || d.M > 4 || d.K % 32 != 0 || d.K > (1 << 20) || d.N * rstride + 16 >= ((int64_t)1 << 31) ||
+      ldx % 4 != 0 || (uintptr_t)d.w % 16 != 0 || (uintptr_t)d.x % 16 != 0)
     return 0;
   const int64_t chunks = (d.bpr + 15 + 15) / 16;  // worst-case skew included
   int c = 2;
@@ -522,6 +536,32 @@ __global__ void ggml_epilogue_kernel(float* __restrict__ y, const float* __restr
   }
 }
 
+// The K segment of the decode GEMV for these rows: the whole row where it fits (row bytes up to
+// 8 chunks per lane, the rows of x within the LDS), else the longest of ceil(blocks / s) blocks,
+// s = 2, 3, ... 64, that fits; 0 if none does.  Segment j runs as its own launch over bytes
+// j * seg of every row and the matching x columns, adding its sums to the output the earlier
+// segments wrote (in segment order); the last applies the bias and the activation.  Without it
+// rows past 8 KB, or longer rows of x than the LDS holds (two rows at K = 14336), took the
+// dequantise + matrix-core path: 150-160 us per call for one or two rows of [14336] x 4096 rows
+// against about 20 us for the GEMV.
+static int64_t ggml_gemv_kseg(const GgmlDesc& d) {
+  int ch, wv;
+  if (ggml_gemv_lds(d, &ch, &wv)) return d.K;
+  const int vpb = ggml_vpb(d.type), bpb = ggml_bpb(d.type);
+  if (!vpb || d.K % vpb != 0) return 0;
+  const int64_t blocks = d.K / vpb;
+  for (int64_t sg = 2; sg <= 64 && sg <= blocks; ++sg) {
+    const int64_t nb = (blocks + sg - 1) / sg;
+    GgmlDesc g = d;
+    g.K = nb * vpb;
+    g.bpr = nb * bpb;
+    g.ldx = d.K;
+    g.row_stride = d.bpr;
+    if (ggml_gemv_lds(g, &ch, &wv)) return g.K;
+  }
+  return 0;
+}
+
 enum class GPlan { kEmpty, kGemv, kDequant, kExact };
 
 static GPlan ggml_plan(const mx_backend* b, const GgmlDesc& d) {
@@ -532,9 +572,10 @@ static GPlan ggml_plan(const mx_backend* b, const GgmlDesc& d) {
   if (d.M <= 4 && ggml_gemv_lds(d, &ch, &wv)) return GPlan::kGemv;
   // Problems this small keep the reference's order (bit-identical).
   if (d.M * d.K * d.N <= ((int64_t)1 << 24)) return GPlan::kExact;
+  if (d.M <= 4 && ggml_gemv_kseg(d)) return GPlan::kGemv;  // in K segments
   GgmlDesc g4 = d;
   g4.M = 4;
-  const bool gemv4 = ggml_gemv_lds(g4, &ch, &wv) != 0;
+  const bool gemv4 = ggml_gemv_kseg(g4) != 0;
   // The weights read once per group of four rows (about 27 us a group at [4096] x 11008 rows),
   // until one dequantisation and a matrix-core contraction (about 143 us there past 16 rows)
   // cost less; both scale with the weight bytes, so the crossover holds across shapes.
@@ -562,29 +603,46 @@ int ggml_dense_run(mx_backend* b, const GgmlDesc& d) {
     case GPlan::kEmpty:
       return MX_OK;
     case GPlan::kGemv: {
-      // Groups of up to four rows, one launch each.
+      // Groups of up to four rows, one launch each per K segment.
+      const int vpb = ggml_vpb(d.type), bpb = ggml_bpb(d.type);
       for (int64_t m0 = 0; m0 < d.M; m0 += 4) {
-        GgmlDesc g = d;
-        g.x = d.x + m0 * d.K;
-        g.out = d.out + m0 * d.N;
-        g.M = std::min<int64_t>(4, d.M - m0);
-        int ch = 0;
-        int waves = 8;
-        const size_t lds = ggml_gemv_lds(g, &ch, &waves);
-        if (!lds) return set_error(MX_ERR_INVALID, "internal: GGML GEMV plan without a launch");
-        // As many workgroups as are resident at once: 16 waves per CU (four per SIMD at up to 128
-        // registers), fewer where LDS runs out.
-        const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(16 / waves, (int64_t)(160 * 1024) / (int64_t)lds));
-        const int grid = (int)std::min<int64_t>((g.N + waves - 1) / waves, per_cu * std::max(b->num_cus, 1));
-        MX_TRY(launch(b, "ggml_gemv", [&] {
-          switch (g.type) {
-            case MX_GGML_Q4_0: launch_gemv_t<MX_GGML_Q4_0>(g, grid, lds, ch, waves, st); break;
-            case MX_GGML_Q8_0: launch_gemv_t<MX_GGML_Q8_0>(g, grid, lds, ch, waves, st); break;
-            case MX_GGML_IQ4_NL: launch_gemv_t<MX_GGML_IQ4_NL>(g, grid, lds, ch, waves, st); break;
-            case MX_GGML_Q4_K: launch_gemv_t<MX_GGML_Q4_K>(g, grid, lds, ch, waves, st); break;
-            default: launch_gemv_t<MX_GGML_Q6_K>(g, grid, lds, ch, waves, st); break;
+        GgmlDesc rows = d;
+        rows.x = d.x + m0 * d.K;
+        rows.out = d.out + m0 * d.N;
+        rows.M = std::min<int64_t>(4, d.M - m0);
+        const int64_t kseg = ggml_gemv_kseg(rows);
+        if (!kseg || (kseg < d.K && !vpb)) return set_error(MX_ERR_INVALID, "internal: GGML GEMV plan without a launch");
+        for (int64_t k0 = 0; k0 < d.K; k0 += kseg) {
+          GgmlDesc g = rows;
+          if (kseg < d.K) {
+            const int64_t kl = std::min<int64_t>(kseg, d.K - k0);
+            g.x = rows.x + k0;
+            g.ldx = d.K;
+            g.K = kl;
+            g.bpr = kl / vpb * bpb;
+            g.row_stride = d.bpr;
+            g.row_off = k0 / vpb * bpb;
+            g.accumulate = k0 > 0;
+            g.epilogue = k0 + kl >= d.K;
           }
-        }));
+          int ch = 0;
+          int waves = 8;
+          const size_t lds = ggml_gemv_lds(g, &ch, &waves);
+          if (!lds) return set_error(MX_ERR_INVALID, "internal: GGML GEMV plan without a launch");
+          // As many workgroups as are resident at once: 16 waves per CU (four per SIMD at up to 128
+          // registers), fewer where LDS runs out.
+          const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(16 / waves, (int64_t)(160 * 1024) / (int64_t)lds));
+          const int grid = (int)std::min<int64_t>((g.N + waves - 1) / waves, per_cu * std::max(b->num_cus, 1));
+          MX_TRY(launch(b, "ggml_gemv", [&] {
+            switch (g.type) {
+              case MX_GGML_Q4_0: launch_gemv_t<MX_GGML_Q4_0>(g, grid, lds, ch, waves, st); break;
+              case MX_GGML_Q8_0: launch_gemv_t<MX_GGML_Q8_0>(g, grid, lds, ch, waves, st); break;
+              case MX_GGML_IQ4_NL: launch_gemv_t<MX_GGML_IQ4_NL>(g, grid, lds, ch, waves, st); break;
+              case MX_GGML_Q4_K: launch_gemv_t<MX_GGML_Q4_K>(g, grid, lds, ch, waves, st); break;
+              default: launch_gemv_t<MX_GGML_Q6_K>(g, grid, lds, ch, waves, st); break;
+            }
+          }));
+        }
       }
       return MX_OK;
     }

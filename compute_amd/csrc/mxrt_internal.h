@@ -262,6 +262,12 @@ struct GgmlDesc {
   float* out;          // [M, N]
   int64_t M = 0, K = 0, N = 0, bpr = 0;
   int type = 0, act = 0;
+  // Decode GEMV over one K segment of longer rows: x rows ldx floats apart (0: K), weight rows
+  // row_stride bytes apart (0: bpr) with the segment's bpr bytes starting row_off bytes into
+  // each; accumulate adds the sums to out (the earlier segments'), epilogue applies the bias and
+  // activation (the last segment).
+  int64_t ldx = 0, row_stride = 0, row_off = 0;
+  int accumulate = 0, epilogue = 1;
 };
 struct GgmlEmbedDesc {
   const uint8_t* data;  // [vocab, bpr]

@@ -3,7 +3,8 @@
 - ggml_dense_exact (problems of at most 2^24 multiply-adds past 4 rows, anything the GEMV does
   not take, and every size under the exact backend option): bit-identical f32 output, bias and
   activation included (the reference's order: dot, then bias, then activation).
-- ggml_gemv (M <= 4, and M <= 20 as one launch per group of four rows): f32 accumulation bar —
+- ggml_gemv (M <= 4, and M <= 20 as one launch per group of four rows; rows too long for one
+  launch in K segments added in order): f32 accumulation bar —
   |y - exact| <= 1e-5 * sum|x*w| per output (the kernel sums in another order), identical bits
   on repeated calls, rows whose byte length is not a multiple of 16 (staging skew), the decode
   shape [1, 4096] x 11008 rows, ragged last groups (M = 5, 15).
@@ -198,6 +199,50 @@ def test_gemv_decode_shape(backend, t):
     r = GgmlRun(backend, t, x, w, b)
     assert r.plan() == "ggml_gemv"
     accumulation_check(r.run(), x, w, t, b)
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("M,K,N", [(1, 14336, 1200), (2, 14336, 600), (3, 14336, 420), (7, 8192, 300)])
+def test_gemv_long_rows_in_k_segments(backend, t, M, K, N):
+    """Rows longer than the GEMV holds at once (row bytes past 8 per lane, or rows of x past the
+    LDS) run as K segments whose sums are added to the output in order; bias once, at the end."""
+    assert M * K * N > 1 << 24
+    x, w, b = problem(t, M, K, N)
+    r = GgmlRun(backend, t, x, w, b)
+    assert r.plan() == "ggml_gemv"
+    got = r.run()
+    accumulation_check(got, x, w, t, b)
+    assert np.array_equal(got.view(np.uint32), r.run().view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [ca.GGMLQ4_0, ca.GGMLQ6_K])
+def test_gemv_k_segments_activation_after_the_last(backend, t):
+    # The activation of the whole sum: applied once, by the last segment's launch.
+    x, w, b = problem(t, 2, 14336, 640)
+    r = GgmlRun(backend, t, x, w, b, ca.ActivationSilu)
+    assert r.plan() == "ggml_gemv"
+    exact, ab = O.ggml_dense_f64(x, w, int(t), b)
+    want = exact * expit(exact)
+    err = np.abs(r.run().astype(np.float64) - want)
+    bound = 1.2 * 1e-5 * ab + 4 * np.finfo(np.float32).eps * np.abs(want) + 1e-30
+    assert (err <= bound).all(), f"worst {np.max(err / bound)} x the bound"
+
+
+def test_gemv_k_segments_noalloc(backend):
+    # The allocation-free entry point takes the same segments (the output is their accumulator).
+    t = ca.GGMLQ6_K
+    x, w, b = problem(t, 1, 14336, 1200)
+    r = GgmlRun(backend, t, x, w, b)
+    out = backend.BufferFromFlatData(0, np.full(1200, np.nan, np.float32), ca.Shape(ca.Float32, 1, 1200))
+    a = _lib.mx_qdense_args()
+    a.x, a.w, a.out = r.inputs[0].DevicePtr(), r.inputs[1].DevicePtr(), out.DevicePtr()
+    a.bias, a.bias_dtype = r.inputs[2].DevicePtr(), O.DT_FLOAT32
+    a.M, a.K, a.N = 1, 14336, 1200
+    a.x_dtype, a.scheme, a.ggml_type, a.activation = O.DT_FLOAT32, int(ca.QuantGGML), int(t), 0
+    assert backend.QDensePlan(a) == "ggml_gemv"
+    backend.QDenseNoAlloc(a)
+    got = out.ToFlatData().reshape(1, 1200)
+    assert np.array_equal(got.view(np.uint32), r.run().view(np.uint32))
 
 
 def embed_graph(backend, t, data, idx, idx_dtype):
