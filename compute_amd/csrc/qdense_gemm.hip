@@ -192,8 +192,11 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
 // are folded into the total with the scales of the block's group at the block's end, so there is
 // no clearing and no per-block branch (a group of G = 64 j rows is folded j times, once per
 // block).  Otherwise groups are counted at run time and the sums cleared after each fold.
-template <int BK, bool GRP, bool FB = false>
+// H (with FB): scale groups of 32 rows, two per 64-row block: each step's sums start from zero and
+// are folded with their own group's scales (after step 0 and at the block's end).
+template <int BK, bool GRP, bool FB = false, bool H = false>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
+  static_assert(!H || (GRP && FB), "32-row groups: bf16 group scales");
   constexpr int PF = kPf;
   // With scale groups the tile is 256 x 64: each wave keeps two of the four interleaved MFMA
   // column sets (columns 4*cg + 2*wc + c, c = 0, 1), which halves both accumulator sets so that
@@ -242,7 +245,8 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       const int kbeg = half * (a.K / kBK / 2);
       a.x += (size_t)kbeg * kBK;
       a.w += k4B<BK> ? (size_t)kbeg * kBK * N / 2 : (size_t)kbeg * kBK * N;
-      if (a.gpb > 0) a.scale = (const char*)a.scale + (size_t)(kbeg / a.gpb) * N * (a.s_dt == MX_DTYPE_FLOAT32 ? 4 : 2);
+      if (a.gpb > 0)
+        a.scale = (const char*)a.scale + (size_t)(kbeg / a.gpb) * (H ? 2 : 1) * N * (a.s_dt == MX_DTYPE_FLOAT32 ? 4 : 2);
       a.K /= 2;
     }
   }
@@ -374,12 +378,16 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   const int lcol = n0 + 64 * wc + 4 * cg;
   const int scol = min(lcol, a.N - NC);
   float sg[NC];
-  u32x2_v sgw = {0u, 0u};
+  u32x2_v sgw = {0u, 0u}, sgw2 = {0u, 0u};
 #pragma unroll
   for (int c = 0; c < NC; ++c) sg[c] = 0.f;
   auto load_sg = [&](int g) __attribute__((always_inline)) {
     g = min(g, a.K / (kBK * max(a.gpb, 1)) - 1);
-    if constexpr (FB) {
+    if constexpr (H) {
+      // The block's two scale rows (groups 2g and 2g + 1).
+      sgw = *(const u32x2_v*)((const uint16_t*)a.scale + (size_t)(2 * g) * N + scol);
+      sgw2 = *(const u32x2_v*)((const uint16_t*)a.scale + (size_t)(2 * g + 1) * N + scol);
+    } else if constexpr (FB) {
       // bf16 scales (the host takes these kernels for bf16 scales only): one 8-byte load, kept
       // as loaded until the fold.
       sgw = *(const u32x2_v*)((const uint16_t*)a.scale + (size_t)g * N + scol);
@@ -420,12 +428,13 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   };
   // End of a scale group (every block with FB): acc += accg * s (this lane's columns; accg = 0
   // unless the next group's first MFMAs start from zero), then the scales of group g_next.
-  auto fold = [&](int g_next) __attribute__((always_inline)) {
+  // acc += accg * s with the bf16 scales of one loaded scale row (FB), or the f32 scales in sg.
+  auto fold_sums = [&](const u32x2_v& w) __attribute__((always_inline)) {
     if constexpr (FB) {
-      sg[0] = __uint_as_float(sgw[0] << 16);
-      sg[1] = __uint_as_float(sgw[0] & 0xFFFF0000u);
-      sg[2] = __uint_as_float(sgw[1] << 16);
-      sg[3] = __uint_as_float(sgw[1] & 0xFFFF0000u);
+      sg[0] = __uint_as_float(w[0] << 16);
+      sg[1] = __uint_as_float(w[0] & 0xFFFF0000u);
+      sg[2] = __uint_as_float(w[1] << 16);
+      sg[3] = __uint_as_float(w[1] & 0xFFFF0000u);
     }
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
@@ -435,6 +444,9 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
         for (int r = 0; r < 4; ++r) acc[rb][c][r] = __builtin_fmaf(accg[rb][c][r], sg[c], acc[rb][c][r]);
         if constexpr (!FB) accg[rb][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
+  };
+  auto fold = [&](int g_next) __attribute__((always_inline)) {
+    fold_sums(H ? sgw2 : sgw);  // H: the block's second group (its first was folded after step 0)
     load_sg(g_next);
   };
 
@@ -472,13 +484,17 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (H) {
+      fold_sums(sgw);  // the block's first 32-row group
+      __builtin_amdgcn_sched_barrier(0);
+    }
     wait_vm<(XB - 2) * (kWGl + kXDma)>();  // this wave's x loads of block kb + 1 are in LDS
     lds_barrier();
     read_step(xb1, B ^ 1, 0, A0, B0);
     store_w(wr4[S2], B);
     load_w(kb + PF, wr4[S]);
     dma_x(kb + XB);
-    mma_step(A1, B1, Acc{});
+    mma_step(A1, B1, std::integral_constant<bool, H>{});  // H: the second group starts from zero
 #pragma unroll
     for (int i = 0; i < 4 + NC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
@@ -622,8 +638,10 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 bool qdense_gemm_fits(const QDenseDesc& d) {
   auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
   const bool per_channel = d.block_axis == 0 && d.block_size >= d.K;
-  // Scale groups of whole 64-row blocks that tile K exactly.
-  const bool grouped = d.block_axis == 0 && d.block_size < d.K && d.block_size % kBK == 0 && d.K % d.block_size == 0;
+  // Scale groups of whole 64-row blocks that tile K exactly, or bf16-scaled groups of 32 rows
+  // (two per block).
+  const bool grouped = d.block_axis == 0 && d.block_size < d.K && d.K % d.block_size == 0 &&
+                       (d.block_size % kBK == 0 || (d.block_size == 32 && d.s_dt == MX_DTYPE_BFLOAT16));
   const bool wt = d.w_dt == MX_DTYPE_INT8 || d.w_dt == MX_DTYPE_UINT8 || d.w_dt == MX_DTYPE_INT4 ||
                   d.w_dt == MX_DTYPE_UINT4;
   return d.M > 16 && d.x_dt == MX_DTYPE_BFLOAT16 && d.scheme == MX_QUANT_LINEAR && !d.zp && (per_channel || grouped) &&
@@ -654,7 +672,9 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.tiles_n = (int)tiles_n;
   ga.grouped = (tiles_m % 2 == 0 && tiles_n % 16 == 0) ? 1 : 0;
   ga.tiles = (int)(tiles_m * tiles_n);
-  ga.gpb = grouped ? (int)(d.block_size / kBK) : 0;
+  // Groups of 32 rows (bf16 scales): one block per pair of groups, each step folded on its own.
+  const bool half = grouped && d.block_size == 32;
+  ga.gpb = half ? 1 : grouped ? (int)(d.block_size / kBK) : 0;
   // Split tail: when the tiles leave a last partial round of at most half the CUs (planned for
   // MI355X's 256 CUs whatever the device reports, so the summation order depends on the shape
   // only), those tiles are computed as two halves of K by twice as many workgroups.  Not under
@@ -678,7 +698,9 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   // bf16 group scales: the fold-every-block kernel; f32 group scales count blocks at run time.
   auto grouped_kernel = [&](auto kind) {
     constexpr int BK = decltype(kind)::value;
-    if (d.s_dt == MX_DTYPE_BFLOAT16)
+    if (half)
+      dispatch(qdense_gemm_kernel<BK, true, true, true>, grid, kThreads, 0, st, ga);
+    else if (d.s_dt == MX_DTYPE_BFLOAT16)
       dispatch(qdense_gemm_kernel<BK, true, true>, grid, kThreads, 0, st, ga);
     else
       dispatch(qdense_gemm_kernel<BK, true>, grid, kThreads, 0, st, ga);

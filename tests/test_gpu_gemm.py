@@ -73,11 +73,12 @@ def test_gemm_small_batch_rows(backend, M):
 
 
 # ---------------------------------------------------------------------------------------------
-# 4-bit weights and K-grouped scales (scale [K/G, N], G a multiple of 64): the same GEMM with the
-# nibbles converted into the LDS tile and a per-group accumulator folded with the group's scales.
+# 4-bit weights and K-grouped scales (scale [K/G, N], G a multiple of 64, or 32 with bf16
+# scales): the same GEMM with the nibbles converted into the LDS tile and a per-group accumulator
+# folded with the group's scales (twice per 64-row block for G = 32).
 # ---------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("w_dtype", [O.DT_INT4, O.DT_UINT4, O.DT_INT8, O.DT_UINT8])
-@pytest.mark.parametrize("G", [None, 64, 128, 256])
+@pytest.mark.parametrize("G", [None, 32, 64, 128, 256])
 def test_gemm_4bit_and_groups(backend, w_dtype, G):
     M, K, N = 300, 512, 272
     p = O.make_problem(M, K, N, w_dtype=w_dtype, block_axis=0, block_size=G if G else K, per_channel_1d=G is None,
@@ -108,7 +109,7 @@ def test_gemm_grouped_activations(backend, act):
     check_rows(r, what=f"act {act}")
 
 
-@pytest.mark.parametrize("w_dtype,G", [(O.DT_INT4, 128), (O.DT_INT8, 64)])
+@pytest.mark.parametrize("w_dtype,G", [(O.DT_INT4, 128), (O.DT_INT8, 64), (O.DT_INT4, 32)])
 def test_gemm_grouped_prefill_full_size(backend, w_dtype, G):
     """x bf16 [2048,4096] x Int4 [4096,14336] g128 (the MLP's gate/up weights at prefill) and the
     int8 g64 layout of BASELINE configs[2] at the same size: 128 seeded rows against the oracle,
@@ -124,7 +125,8 @@ def test_gemm_grouped_prefill_full_size(backend, w_dtype, G):
 
 @pytest.mark.parametrize("w_dtype,G,s_dtype,act", [(O.DT_INT8, None, O.DT_FLOAT32, O.ACT_GELU),
                                                     (O.DT_INT4, 128, O.DT_FLOAT32, O.ACT_NONE),
-                                                    (O.DT_UINT4, 64, O.DT_BFLOAT16, O.ACT_SILU)])
+                                                    (O.DT_UINT4, 64, O.DT_BFLOAT16, O.ACT_SILU),
+                                                    (O.DT_INT4, 32, O.DT_BFLOAT16, O.ACT_NONE)])
 def test_gemm_split_tail(backend, w_dtype, G, s_dtype, act):
     """272 tiles of 256 x 128 (x [512, 1024], N = 17408): the 16 tiles past the last whole round of
     256 are computed as two halves of K whose partial tiles the second half adds (per-channel
