@@ -193,10 +193,12 @@ __device__ __forceinline__ void store_tile(const f32x4_t (&acc)[4][4], const flo
 // no clearing and no per-block branch (a group of G = 64 j rows is folded j times, once per
 // block).  Otherwise groups are counted at run time and the sums cleared after each fold.
 // H (with FB): scale groups of 32 rows, two per 64-row block: each step's sums start from zero and
-// are folded with their own group's scales (after step 0 and at the block's end).
-template <int BK, bool GRP, bool FB = false, bool H = false>
+// are folded with their own group's scales (after step 0 and at the block's end); HF: those
+// scales in f32 (else bf16).
+template <int BK, bool GRP, bool FB = false, bool H = false, bool HF = false>
 __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
-  static_assert(!H || (GRP && FB), "32-row groups: bf16 group scales");
+  static_assert(!H || (GRP && FB), "32-row groups: the fold-every-step form");
+  static_assert(!HF || H, "f32 scales for 32-row groups only");
   constexpr int PF = kPf;
   // With scale groups the tile is 256 x 64: each wave keeps two of the four interleaved MFMA
   // column sets (columns 4*cg + 2*wc + c, c = 0, 1), which halves both accumulator sets so that
@@ -379,11 +381,16 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   const int scol = min(lcol, a.N - NC);
   float sg[NC];
   u32x2_v sgw = {0u, 0u}, sgw2 = {0u, 0u};
+  f32x4_t sgf = {0.f, 0.f, 0.f, 0.f}, sgf2 = sgf;  // HF: the block's two rows of f32 scales
 #pragma unroll
   for (int c = 0; c < NC; ++c) sg[c] = 0.f;
   auto load_sg = [&](int g) __attribute__((always_inline)) {
     g = min(g, a.K / (kBK * max(a.gpb, 1)) - 1);
-    if constexpr (H) {
+    if constexpr (HF) {
+      // The block's two scale rows (groups 2g and 2g + 1), one 16-byte load each.
+      sgf = *(const f32x4_t*)((const float*)a.scale + (size_t)(2 * g) * N + scol);
+      sgf2 = *(const f32x4_t*)((const float*)a.scale + (size_t)(2 * g + 1) * N + scol);
+    } else if constexpr (H) {
       // The block's two scale rows (groups 2g and 2g + 1).
       sgw = *(const u32x2_v*)((const uint16_t*)a.scale + (size_t)(2 * g) * N + scol);
       sgw2 = *(const u32x2_v*)((const uint16_t*)a.scale + (size_t)(2 * g + 1) * N + scol);
@@ -429,8 +436,11 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
   // End of a scale group (every block with FB): acc += accg * s (this lane's columns; accg = 0
   // unless the next group's first MFMAs start from zero), then the scales of group g_next.
   // acc += accg * s with the bf16 scales of one loaded scale row (FB), or the f32 scales in sg.
-  auto fold_sums = [&](const u32x2_v& w) __attribute__((always_inline)) {
-    if constexpr (FB) {
+  auto fold_sums = [&](const u32x2_v& w, const f32x4_t& wf) __attribute__((always_inline)) {
+    if constexpr (HF) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) sg[c] = wf[c];
+    } else if constexpr (FB) {
       sg[0] = __uint_as_float(w[0] << 16);
       sg[1] = __uint_as_float(w[0] & 0xFFFF0000u);
       sg[2] = __uint_as_float(w[1] << 16);
@@ -446,7 +456,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
       }
   };
   auto fold = [&](int g_next) __attribute__((always_inline)) {
-    fold_sums(H ? sgw2 : sgw);  // H: the block's second group (its first was folded after step 0)
+    fold_sums(H ? sgw2 : sgw, sgf2);  // H: the block's second group (its first was folded after step 0)
     load_sg(g_next);
   };
 
@@ -485,7 +495,7 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (H) {
-      fold_sums(sgw);  // the block's first 32-row group
+      fold_sums(sgw, sgf);  // the block's first 32-row group
       __builtin_amdgcn_sched_barrier(0);
     }
     wait_vm<(XB - 2) * (kWGl + kXDma)>();  // this wave's x loads of block kb + 1 are in LDS
@@ -638,10 +648,12 @@ __global__ __launch_bounds__(kThreads) void qdense_gemm_kernel(GemmArgs a) {
 bool qdense_gemm_fits(const QDenseDesc& d) {
   auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
   const bool per_channel = d.block_axis == 0 && d.block_size >= d.K;
-  // Scale groups of whole 64-row blocks that tile K exactly, or bf16-scaled groups of 32 rows
-  // (two per block).
+  // Scale groups of whole 64-row blocks that tile K exactly, or groups of 32 rows (two per
+  // block).  The group kernels load a lane's four scales as one vector (bf16: 8 bytes, f32 groups
+  // of 32: 16 bytes), from a 16-byte-aligned scale array.
   const bool grouped = d.block_axis == 0 && d.block_size < d.K && d.K % d.block_size == 0 &&
-                       (d.block_size % kBK == 0 || (d.block_size == 32 && d.s_dt == MX_DTYPE_BFLOAT16));
+                       (d.block_size % kBK == 0 || d.block_size == 32) &&
+                       (aligned(d.scale, 16) || (d.s_dt == MX_DTYPE_FLOAT32 && d.block_size != 32));
   const bool wt = d.w_dt == MX_DTYPE_INT8 || d.w_dt == MX_DTYPE_UINT8 || d.w_dt == MX_DTYPE_INT4 ||
                   d.w_dt == MX_DTYPE_UINT4;
   return d.M > 16 && d.x_dt == MX_DTYPE_BFLOAT16 && d.scheme == MX_QUANT_LINEAR && !d.zp && (per_channel || grouped) &&
@@ -698,7 +710,9 @@ int qdense_gemm_run(mx_backend* b, const QDenseDesc& d, const char* name) {
   // bf16 group scales: the fold-every-block kernel; f32 group scales count blocks at run time.
   auto grouped_kernel = [&](auto kind) {
     constexpr int BK = decltype(kind)::value;
-    if (half)
+    if (half && d.s_dt == MX_DTYPE_FLOAT32)
+      dispatch(qdense_gemm_kernel<BK, true, true, true, true>, grid, kThreads, 0, st, ga);
+    else if (half)
       dispatch(qdense_gemm_kernel<BK, true, true, true>, grid, kThreads, 0, st, ga);
     else if (d.s_dt == MX_DTYPE_BFLOAT16)
       dispatch(qdense_gemm_kernel<BK, true, true>, grid, kThreads, 0, st, ga);

@@ -370,13 +370,12 @@ def test_qdense_plan_selection():
             assert _plan(b, 2048, 4096, 14336, x_dtype=BF16, w_dtype=ca.Int8, s_dtype=BF16, block_axis=0,
                          block_size=64) == want("qdense_gemm_mfma_i8_grouped")
             # Groups that do not tile K in 64-row blocks take the f32 dequantise-and-contract path,
-            # except bf16-scaled groups of 32 rows (two per block, each step folded).
+            # except groups of 32 rows (two per block, each step folded).
             assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
                          block_size=96) == want("qdense_refgemm_f32_mfma")
-            assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
-                         block_size=32) == want("qdense_gemm_mfma_i4_grouped")
-            assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=F32, block_axis=0,
-                         block_size=32) == want("qdense_refgemm_f32_mfma")
+            for s_dt in (BF16, F32):
+                assert _plan(b, 2048, 4096, 4096, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=s_dt, block_axis=0,
+                             block_size=32) == want("qdense_gemm_mfma_i4_grouped")
             # Small problems, M > 64 with the reference layout, unsupported block sizes: reference order.
             assert _plan(b, 1, 512, 1024, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=64) == "qdense_exact"

@@ -90,7 +90,7 @@ def test_gemm_4bit_and_groups(backend, w_dtype, G):
     assert np.array_equal(r.run(), r.run())
 
 
-@pytest.mark.parametrize("shape", [(17, 128, 16, 64), (1000, 1024, 4112, 128), (513, 2048, 1040, 512)])
+@pytest.mark.parametrize("shape", [(17, 128, 16, 64), (1000, 1024, 4112, 128), (513, 2048, 1040, 512), (300, 512, 272, 32)])
 def test_gemm_grouped_shapes(backend, shape):
     M, K, N, G = shape
     p = O.make_problem(M, K, N, w_dtype=O.DT_INT4, block_axis=0, block_size=G, scale_dtype=O.DT_FLOAT32,
@@ -126,7 +126,8 @@ def test_gemm_grouped_prefill_full_size(backend, w_dtype, G):
 @pytest.mark.parametrize("w_dtype,G,s_dtype,act", [(O.DT_INT8, None, O.DT_FLOAT32, O.ACT_GELU),
                                                     (O.DT_INT4, 128, O.DT_FLOAT32, O.ACT_NONE),
                                                     (O.DT_UINT4, 64, O.DT_BFLOAT16, O.ACT_SILU),
-                                                    (O.DT_INT4, 32, O.DT_BFLOAT16, O.ACT_NONE)])
+                                                    (O.DT_INT4, 32, O.DT_BFLOAT16, O.ACT_NONE),
+                                                    (O.DT_UINT8, 32, O.DT_FLOAT32, O.ACT_GELU)])
 def test_gemm_split_tail(backend, w_dtype, G, s_dtype, act):
     """272 tiles of 256 x 128 (x [512, 1024], N = 17408): the 16 tiles past the last whole round of
     256 are computed as two halves of K whose partial tiles the second half adds (per-channel
