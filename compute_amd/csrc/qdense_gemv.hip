@@ -64,9 +64,10 @@ struct GemvArgs {
   const void* zp;      // [K, nblk] or null
   const void* bias;    // [N] or null
   void* out;           // [M, N], dtype of x
-  float* partial;      // [S, M, N] (S > 1)
+  float* partial;      // [S, M, Np] (S > 1)
   uint32_t* counters;  // [column blocks], zero between launches
   int M, K, N, B, S, nblk, act, x_dt, s_dt, zp_dt, b_dt;
+  int Np;              // the partial tiles' row stride: N rounded up to 4
 };
 
 __device__ __forceinline__ int gv_xcd_swizzle(int bid, int total) {
@@ -113,7 +114,10 @@ __device__ __forceinline__ void gv_pin(float (&v)[MR]) {
 // folded into x row by row).  0: blocks of B rows along K, [ceil(K/B), N] (B % 32 == 0 or B >= K,
 // so a wave's 32 rows share one group: the wave sums x*w' and x over its rows and applies its
 // columns' scale and zero point once).
-template <int WK, int MR, int AX, int WV = kGvWaves>
+// UN: rows that start mid-word (N % 8 != 0 for 4-bit weights, N % 4 != 0 for 8-bit ones, K * N
+// < 2^31): each lane's word of a row is read as the two aligned words that hold it and a funnel
+// shift.
+template <int WK, int MR, int AX, int WV = kGvWaves, bool UN = false>
 __global__ __launch_bounds__(64 * WV) void qdense_gemv_kernel(GemvArgs a) {
   constexpr int kWv = WV, kThr = 64 * WV, kSlice = kGvRows * WV;
   constexpr bool k4 = WK == kGvI4 || WK == kGvU4 || WK == kGvNF4;
@@ -191,10 +195,31 @@ __global__ __launch_bounds__(64 * WV) void qdense_gemv_kernel(GemvArgs a) {
   // past K read row K-1 (their x is 0).
   const uint8_t* wp = a.w + (lbyte + 4 <= row_bytes ? lbyte : 0);
   // Issued in row order (the rows are computed in that order and loads complete in order).
-  uint32_t wv[kGvRows];
+  uint32_t wv[kGvRows], wh[UN ? kGvRows : 1];
+  // UN: element e = k * N + e0 of the flattened weights (a nibble index for 4-bit weights) is the
+  // lane's first; the words are read through a buffer range of the array's size rounded up to 4
+  // bytes (the allocation's granule holds those bytes), lanes past N read column 0.
+  const uint32_t e0 = col0 < a.N ? (uint32_t)col0 : 0u;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.w), (short)0,
+      UN ? (int)((((uint32_t)a.K * (uint32_t)a.N + (k4 ? 1u : 0u)) / (k4 ? 2u : 1u) + 3u) & ~3u) : 0, 0x00020000);
+  auto un_byte = [&](int r) {
+    const uint32_t e = (uint32_t)min(kw + r, a.K - 1) * (uint32_t)a.N + e0;
+    return k4 ? e >> 1 : e;
+  };
+  auto un_shift = [&](int r) {
+    const uint32_t e = (uint32_t)min(kw + r, a.K - 1) * (uint32_t)a.N + e0;
+    return ((k4 ? e >> 1 : e) & 3u) * 8u + (k4 ? (e & 1u) * 4u : 0u);
+  };
 #pragma unroll
   for (int r = 0; r < kGvRows; ++r) {
-    wv[r] = __builtin_nontemporal_load((const uint32_t*)(wp + (size_t)min(kw + r, a.K - 1) * row_bytes));
+    if constexpr (UN) {
+      const uint32_t b4 = un_byte(r) & ~3u;
+      wv[r] = __builtin_amdgcn_raw_buffer_load_b32(wrs, b4, 0, 0);
+      wh[r] = __builtin_amdgcn_raw_buffer_load_b32(wrs, b4 + 4u, 0, 0);
+    } else {
+      wv[r] = __builtin_nontemporal_load((const uint32_t*)(wp + (size_t)min(kw + r, a.K - 1) * row_bytes));
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -240,7 +265,7 @@ __global__ __launch_bounds__(64 * WV) void qdense_gemv_kernel(GemvArgs a) {
       for (int m = 0; m < MR; ++m) xs[m] = xr[m];
     }
     float wf[CPL];
-    const uint32_t v = wv[r] ^ kFlip;
+    const uint32_t v = (UN ? __builtin_amdgcn_alignbit(wh[UN ? r : 0], wv[r], un_shift(r)) : wv[r]) ^ kFlip;
     if constexpr (kNF) {
       if constexpr (k4) {
 #pragma unroll
@@ -336,16 +361,16 @@ __global__ __launch_bounds__(64 * WV) void qdense_gemv_kernel(GemvArgs a) {
 
   // Split K: store this slice's tile as [slice][M][N] (16-byte stores with the agent-scope
   // coherence bit sc1), wait until the stores have completed, then count the arrival; only the
-  // last arriver reads the tiles back, with loads that carry the same bit.  N % 4 == 0, so a
-  // quad is whole or past the end.
+  // last arriver reads the tiles back, with loads that carry the same bit.  The tiles' rows are
+  // Np = N rounded up to 4 floats apart, so a quad is whole or past the end.
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-      a.partial, (short)0, (int)((size_t)a.S * M * a.N * sizeof(float)), 0x00020000);
+      a.partial, (short)0, (int)((size_t)a.S * M * a.Np * sizeof(float)), 0x00020000);
   constexpr int kSc1 = 16;  // cache-policy operand of the buffer intrinsics: sc1
   for (int g = t; g < NQ; g += kThr) {
     const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
     if (col < a.N)
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(gv_u32x4, wave_sum(g)), prs,
-                                            (unsigned)(((slice * M + m) * a.N + col) * 4), 0, kSc1);
+                                            (unsigned)(((slice * M + m) * a.Np + col) * 4), 0, kSc1);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -360,7 +385,7 @@ __global__ __launch_bounds__(64 * WV) void qdense_gemv_kernel(GemvArgs a) {
   constexpr int kSl = 16;
   for (int g = t; g < NQ; g += kThr) {
     const int m = g / kQPR, col = cblk + 4 * (g % kQPR);
-    const int c = min(col, a.N - 4);
+    const int c = min(col, a.Np - 4);
     gv_f32x4 y = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int s0 = 0; s0 < a.S; s0 += kSl) {
       gv_f32x4 v[kSl];
@@ -368,7 +393,7 @@ __global__ __launch_bounds__(64 * WV) void qdense_gemv_kernel(GemvArgs a) {
       for (int u = 0; u < kSl; ++u) {
         const int s = min(s0 + u, a.S - 1);
         v[u] = __builtin_bit_cast(gv_f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                prs, (unsigned)(((s * M + m) * a.N + c) * 4), 0, kSc1));
+                                                prs, (unsigned)(((s * M + m) * a.Np + c) * 4), 0, kSc1));
       }
 #pragma unroll
       for (int u = 0; u < kSl; ++u)
@@ -406,13 +431,21 @@ bool qdense_gemv_fits(const QDenseDesc& d) {
   auto aligned = [](const void* p, size_t al) { return ((uintptr_t)p % al) == 0; };
   const bool blocks = d.block_axis == 1 ? d.block_size >= kGvMinBlock && d.block_size % cpl == 0
                                         : d.block_size % kGvRows == 0 || d.block_size >= d.K;
+  // Rows that start mid-word (other N) take the kernel's two-word loads, within 2^31 elements.
   return d.K >= 1 && d.K * d.N >= kGvMinWeights && d.K < (int64_t)1 << 30 && d.N < (int64_t)1 << 30 &&
-         d.N % (packed ? 8 : 4) == 0 && blocks && aligned(d.w, 4) &&
+         (d.N % (packed ? 8 : 4) == 0 || d.K * d.N < ((int64_t)1 << 31)) && blocks && aligned(d.w, 4) &&
          aligned(d.out, d.x_dt == MX_DTYPE_FLOAT32 ? 16 : 8);
 }
 
 template <int WK, int AX>
 static void gemv_launch_ax(const GemvArgs& ga, int waves, int grid, size_t lds, hipStream_t st) {
+  if (ga.N % (WK == kGvI4 || WK == kGvU4 || WK == kGvNF4 ? 8 : 4) != 0) {  // rows start mid-word
+    if (ga.M == 1)
+      dispatch(qdense_gemv_kernel<WK, 1, AX, kGvWaves, true>, grid, kGvThreads, lds, st, ga);
+    else
+      dispatch(qdense_gemv_kernel<WK, kGvMaxRows, AX, kGvWaves, true>, grid, kGvThreads, lds, st, ga);
+    return;
+  }
   if (ga.M == 1 && waves == kGvWavesWide)
     dispatch(qdense_gemv_kernel<WK, 1, AX, kGvWavesWide>, grid, 64 * kGvWavesWide, lds, st, ga);
   else if (ga.M == 1)
@@ -455,12 +488,15 @@ static int gemv_run_rows(mx_backend* b, const QDenseDesc& d, const char* name) {
   // shape only).
   const int64_t S8 = (d.K + kGvSlice - 1) / kGvSlice;
   const int64_t SW = (d.K + kGvRows * kGvWavesWide - 1) / (kGvRows * kGvWavesWide);
-  const int waves = d.M == 1 && nb * S8 > kGvPlanCUs && nb * SW <= kGvPlanCUs && 4 * nb * SW >= 3 * kGvPlanCUs
+  const bool unaligned = d.N % (packed ? 8 : 4) != 0;  // eight-wave kernels only
+  const int waves = !unaligned && d.M == 1 && nb * S8 > kGvPlanCUs && nb * SW <= kGvPlanCUs &&
+                            4 * nb * SW >= 3 * kGvPlanCUs
                         ? kGvWavesWide
                         : kGvWaves;
+  const int64_t Np = (d.N + 3) / 4 * 4;
   const int64_t S = waves == kGvWaves ? S8 : SW;
   const size_t counter_bytes = 64 * 1024;
-  if ((size_t)nb * 4 > counter_bytes || nb * S > (int64_t)1 << 30 || S * d.M * d.N * 4 >= (int64_t)1 << 31)
+  if ((size_t)nb * 4 > counter_bytes || nb * S > (int64_t)1 << 30 || S * d.M * Np * 4 >= (int64_t)1 << 31)
     return set_error(MX_ERR_INVALID, "FusedQuantizedDense: N=%lld too large for the GEMV path", (long long)d.N);
   GemvArgs ga;
   ga.x = d.x;
@@ -473,13 +509,14 @@ static int gemv_run_rows(mx_backend* b, const QDenseDesc& d, const char* name) {
   ga.counters = nullptr;
   if (S > 1) {
     void* scratch = nullptr;
-    MX_TRY(ensure_scratch(b, counter_bytes + (size_t)S * d.M * d.N * sizeof(float), &scratch));
+    MX_TRY(ensure_scratch(b, counter_bytes + (size_t)S * d.M * Np * sizeof(float), &scratch));
     ga.counters = (uint32_t*)scratch;
     ga.partial = (float*)((char*)scratch + counter_bytes);
   }
   ga.M = (int)d.M;
   ga.K = (int)d.K;
   ga.N = (int)d.N;
+  ga.Np = (int)Np;
   ga.B = (int)std::min<int64_t>(d.block_size, d.block_axis == 1 ? d.N : d.K);
   ga.S = (int)S;
   ga.nblk = (int)((d.N + d.block_size - 1) / d.block_size);

@@ -359,6 +359,12 @@ def test_qdense_plan_selection():
                 sfx = "_grouped" if grouped == "gemm_mfma" else ""
                 assert _plan(b, M, 4096, 14336, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
                              block_size=128) == want(f"qdense_{grouped}_i4{sfx}")
+            # Rows that start mid-word (odd N): the GEMV's two-word loads (the MFMA kernels need
+            # aligned rows).
+            assert _plan(b, 1, 4096, 32001, x_dtype=BF16, w_dtype=ca.Int4, s_dtype=BF16, block_axis=0,
+                         block_size=128) == want("qdense_gemv_i4")
+            assert _plan(b, 4, 4096, 32001, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
+                         block_size=128) == want("qdense_gemv_i8")
             # Where the GEMM does not fit (f32 x here), rows up to 64 stay on the GEMV.
             assert _plan(b, 32, 4096, 11008, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
                          block_size=64) == want("qdense_gemv_i8")

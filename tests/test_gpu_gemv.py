@@ -179,3 +179,32 @@ def test_gemv_row_groups(backend, M, w_dtype, scheme, zp):
                        block_axis=1, block_size=128, bias=True, zp=zp, scheme=scheme, seed=990 + M)
     r, y = _run(backend, p)
     _check(p, y)
+
+
+@pytest.mark.parametrize("w_dtype", W_DTYPES)
+@pytest.mark.parametrize("M,K,N,axis,B", [(1, 1024, 1031, 1, 64), (3, 1040, 1235, 0, 64), (1, 4096, 32001, 1, 128),
+                                          (2, 4096, 32001, 0, 128)])
+def test_gemv_rows_starting_mid_word(backend, w_dtype, M, K, N, axis, B):
+    """N not a multiple of 8 (4-bit) or 4 (8-bit): row k of the packed weights starts mid-word
+    (mid-byte for odd N and 4-bit weights); each lane's word is read as two aligned words and a
+    funnel shift.  f32 x in both scale layouts, zero points, bias; split K on the larger ones."""
+    if w_dtype in (O.DT_INT8, O.DT_UINT8) and N % 4 == 0:
+        pytest.skip("aligned rows")
+    p = O.make_problem(M, K, N, w_dtype=w_dtype, x_dtype=O.DT_FLOAT32, scale_dtype=O.DT_FLOAT32,
+                       block_axis=axis, block_size=B, bias=True, zp=True, seed=1300 + N + w_dtype)
+    r, y = _run(backend, p)
+    _check(p, y)
+    assert np.array_equal(y.view(np.uint32), r.run().view(np.uint32))
+
+
+@pytest.mark.parametrize("w_dtype,scheme", [(O.DT_INT4, O.QUANT_LINEAR), (O.DT_UINT4, O.QUANT_NF4),
+                                            (O.DT_INT8, O.QUANT_LINEAR)])
+@pytest.mark.parametrize("M", [1, 6])
+def test_gemv_rows_starting_mid_word_bf16(backend, w_dtype, scheme, M):
+    """bf16 x with K-blocked bf16 scales at an odd width (the MFMA decode kernel needs aligned
+    rows): the GEMV with two-word loads; NF4 codes and row groups past four rows."""
+    p = O.make_problem(M, 2048, 4097, w_dtype=w_dtype, x_dtype=O.DT_BFLOAT16, scale_dtype=O.DT_BFLOAT16,
+                       block_axis=0, block_size=128, bias=True, scheme=scheme, scale_range=(0.002, 0.02),
+                       seed=1400 + M + w_dtype)
+    r, y = _run(backend, p)
+    _check(p, y)
