@@ -389,6 +389,21 @@ static bool skinny_rows_fit(const QDenseDesc& d) {
   return qdense_skinny_fits(g);
 }
 
+// Past the GEMV's 64 rows, for what neither the GEMM nor the fused reference-layout kernel takes
+// (rows that start mid-word: N not a multiple of the 16 columns those kernels load): the GEMV once
+// per group of four rows, which reads the weights again per group.  From 2^24 weights that still
+// beats the exact kernel, whose sequential multiply-adds run at about 3 TMAC/s: Int4 f32 x
+// [4096] x 32001 with [K, 251] scales takes 5.7 ms (128 rows) and 22.9 ms (512 rows) in the exact
+// kernel and about 11 us per row in the GEMV.
+constexpr int64_t kGemvManyRowsMinWeights = (int64_t)1 << 24;
+
+static bool gemv_many_rows_plan(const QDenseDesc& d) {
+  if (d.K * d.N < kGemvManyRowsMinWeights) return false;
+  QDenseDesc g = d;
+  g.M = 1;  // the row count is the only limit qdense_gemv_fits applies past one row
+  return qdense_gemv_fits(g);
+}
+
 static GgmlDesc ggml_desc(const QDenseDesc& d) {
   GgmlDesc g;
   g.x = (const float*)d.x;
@@ -416,6 +431,7 @@ static QPath choose_path(const mx_backend* b, const QDenseDesc& d) {
   if (qdense_gemm_fits(d)) return QPath::kGemm;
   // The reference layout, f32 x, zero points and NF4 at prefill size: the fused kernel.
   if (qdense_refgemm_plan(d)) return QPath::kRefGemm;
+  if (gemv_many_rows_plan(d)) return QPath::kGemv;
   return QPath::kExact;
 }
 

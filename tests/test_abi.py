@@ -365,6 +365,12 @@ def test_qdense_plan_selection():
                          block_size=128) == want("qdense_gemv_i4")
             assert _plan(b, 4, 4096, 32001, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=1,
                          block_size=128) == want("qdense_gemv_i8")
+            # ... past 64 rows as well, once the weights reach 2^24 (the GEMV per four rows beats
+            # the exact kernel there); smaller weights keep the exact kernel.
+            assert _plan(b, 512, 4096, 32001, x_dtype=F32, w_dtype=ca.Int4, s_dtype=F32, block_axis=1,
+                         block_size=128) == want("qdense_gemv_i4")
+            assert _plan(b, 512, 1024, 1031, x_dtype=F32, w_dtype=ca.Int4, s_dtype=F32, block_axis=1,
+                         block_size=64) == want("qdense_exact")
             # Where the GEMM does not fit (f32 x here), rows up to 64 stay on the GEMV.
             assert _plan(b, 32, 4096, 11008, x_dtype=F32, w_dtype=ca.Int8, s_dtype=F32, block_axis=0,
                          block_size=64) == want("qdense_gemv_i8")

@@ -197,6 +197,19 @@ def test_gemv_rows_starting_mid_word(backend, w_dtype, M, K, N, axis, B):
     assert np.array_equal(y.view(np.uint32), r.run().view(np.uint32))
 
 
+@pytest.mark.parametrize("w_dtype,x_dtype,axis", [(O.DT_INT4, O.DT_FLOAT32, 1), (O.DT_UINT8, O.DT_FLOAT32, 0),
+                                                  (O.DT_INT4, O.DT_BFLOAT16, 0)])
+def test_gemv_rows_starting_mid_word_past_64_rows(backend, w_dtype, x_dtype, axis):
+    """Odd N past 64 rows with 2^24 weights: no MFMA kernel takes rows that start mid-word, and
+    the GEMV once per group of four rows replaces the exact kernel (17 groups here, the last of
+    two rows); zero points and bias with f32 x."""
+    f32 = x_dtype == O.DT_FLOAT32
+    p = O.make_problem(66, 4096, 4097, w_dtype=w_dtype, x_dtype=x_dtype, scale_dtype=x_dtype, block_axis=axis,
+                       block_size=128, bias=True, zp=f32, scale_range=(0.002, 0.02), seed=1500 + w_dtype + axis)
+    r, y = _run(backend, p)  # asserts the GEMV plan
+    _check(p, y)
+
+
 @pytest.mark.parametrize("w_dtype,scheme", [(O.DT_INT4, O.QUANT_LINEAR), (O.DT_UINT4, O.QUANT_NF4),
                                             (O.DT_INT8, O.QUANT_LINEAR)])
 @pytest.mark.parametrize("M", [1, 6])
