@@ -158,9 +158,10 @@ typedef uint64_t mx_value;
  * points and NF4 (past 64 rows), and of GGML rows (past 20 rows), also round each term's weight
  * factor w*s (or w*s+zp) before the product with x, where the reference rounds (x*w)*s; they
  * stay within the f32 accumulation bound of the reference's sum.  Below the fast kernels'
- * thresholds (the decode GEMV from 2^20 weights; the f32 dequantise-and-contract paths and the
- * GGML paths past four rows from 2^24 multiply-adds) problems take the reference-order kernel;
- * the bf16-x decode kernel has no threshold.  "gemv_over_gemm" (measurement only:
+ * thresholds (the decode GEMV from 2^20 weights, and past 64 rows, for widths whose packed rows
+ * start mid-word, from 2^24 weights; the f32 dequantise-and-contract paths and the GGML paths
+ * past four rows from 2^24 multiply-adds) problems take the reference-order kernel; the bf16-x
+ * decode kernel has no threshold.  "gemv_over_gemm" (measurement only:
  * bf16 x with 17..64 rows takes the GEMV even where the prefill GEMM fits, which it otherwise
  * prefers). */
 int mx_backend_new(const char* config, mx_backend** out);
